@@ -1,0 +1,25 @@
+"""MI355X-native token-sampling path (drop-in for Forgeline's sampler).
+
+Public API
+----------
+apply_sampling_filters, sample_from_logits, generate_tokens
+    Reference-compatible functions (src/forgeline/models/generation/sampling.py).
+sample_tokens, describe_rows, filtered_outputs
+    Batched entry points with heterogeneous per-row parameters.
+speculative_verify, SpeculativeGenerator
+    Speculative-decoding accept / resample (models/generation/speculative.py).
+SamplingParams
+    Per-request parameters with the reference's validation (inference/requests.py).
+"""
+
+from .params import GenerationSettings, SamplingParams, SamplingParamsError
+from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, describe_rows, filtered_outputs,
+                       generate_tokens, sample_from_logits, sample_tokens)
+from .speculative import SpeculativeGenerator, SpecOutput, speculative_verify
+
+__all__ = [
+    "apply_sampling_filters", "sample_from_logits", "generate_tokens",
+    "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplingError",
+    "speculative_verify", "SpeculativeGenerator", "SpecOutput",
+    "SamplingParams", "GenerationSettings", "SamplingParamsError",
+]

@@ -1,0 +1,107 @@
+// C ABI of libflsampler.so: argument validation and kernel dispatch.
+// Declarations and conventions: include/fl_sampler.h.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "fl_kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return FL_OK;
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(FL_EIO, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+int validate_sample(const fl_sample_args* a, const char* fn) {
+  if (a == nullptr) return fail(FL_EINVAL, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(fl_sample_args))
+    return fail(FL_EINVAL, "%s: struct_size %u != %zu (header/library mismatch)", fn, a->struct_size,
+                sizeof(fl_sample_args));
+  if (a->dtype != FL_DTYPE_F32 && a->dtype != FL_DTYPE_BF16 && a->dtype != FL_DTYPE_F16)
+    return fail(FL_EINVAL, "%s: unknown dtype %d", fn, a->dtype);
+  if (a->batch < 0) return fail(FL_EINVAL, "%s: batch %lld < 0", fn, static_cast<long long>(a->batch));
+  if (a->batch > 0x7fffffff) return fail(FL_ENOTSUP, "%s: batch %lld too large", fn, static_cast<long long>(a->batch));
+  if (a->vocab < 1) return fail(FL_EINVAL, "%s: vocab %lld < 1", fn, static_cast<long long>(a->vocab));
+  const int64_t vmax = a->dtype == FL_DTYPE_F32 ? FL_MAX_VOCAB_F32 : FL_MAX_VOCAB_16;
+  if (a->vocab > vmax)
+    return fail(FL_ENOTSUP, "%s: vocab %lld exceeds this build's limit %lld for dtype %d", fn,
+                static_cast<long long>(a->vocab), static_cast<long long>(vmax), a->dtype);
+  if (a->ld < a->vocab) return fail(FL_EINVAL, "%s: ld %lld < vocab %lld", fn, static_cast<long long>(a->ld),
+                                    static_cast<long long>(a->vocab));
+  if (a->batch > 0 && a->logits == nullptr) return fail(FL_EINVAL, "%s: logits is NULL", fn);
+  if (!(a->softcap >= 0.0f) || std::isinf(a->softcap)) return fail(FL_EINVAL, "%s: softcap must be finite and >= 0", fn);
+  if (a->hist_ids != nullptr && (a->hist_len == nullptr || a->hist_ld < 0))
+    return fail(FL_EINVAL, "%s: hist_ids needs hist_len and hist_ld >= 0", fn);
+  if (a->n_stop < 0 || (a->n_stop > 0 && (a->stop_ids == nullptr || a->stop_ld < 0)))
+    return fail(FL_EINVAL, "%s: stop_ids/n_stop/stop_ld inconsistent", fn);
+  return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_abi_version(void) { return FL_ABI_VERSION; }
+
+const char* fl_last_error(void) { return g_error.c_str(); }
+
+int fl_sample(const fl_sample_args* a, void* stream) {
+  int rc = validate_sample(a, "fl_sample");
+  if (rc != FL_OK) return rc;
+  const bool select = (a->flags & FL_FLAG_NO_SELECT) == 0;
+  if (select && a->out_token == nullptr) return fail(FL_EINVAL, "fl_sample: out_token is NULL");
+  if (a->batch == 0) return ok();
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = a->dtype == FL_DTYPE_F32 ? fl::launch_sample_rows32(*a, s) : fl::launch_sample_rows16(*a, s);
+  return check_launch(e, "fl_sample");
+}
+
+int fl_apply_filter(const fl_sample_args* a, const fl_row_desc* desc, void* out_filtered, int64_t out_ld,
+                    float* out_probs, uint32_t* out_mask, void* stream) {
+  int rc = validate_sample(a, "fl_apply_filter");
+  if (rc != FL_OK) return rc;
+  if (desc == nullptr) return fail(FL_EINVAL, "fl_apply_filter: desc is NULL");
+  if (out_filtered != nullptr && out_ld < a->vocab) return fail(FL_EINVAL, "fl_apply_filter: out_ld < vocab");
+  if (a->batch == 0 || (out_filtered == nullptr && out_probs == nullptr && out_mask == nullptr)) return ok();
+  const hipError_t e =
+      fl::launch_apply_filter(*a, desc, out_filtered, out_ld, out_probs, out_mask, static_cast<hipStream_t>(stream));
+  return check_launch(e, "fl_apply_filter");
+}
+
+int fl_spec_verify(const fl_spec_args* a, void* stream) {
+  if (a == nullptr) return fail(FL_EINVAL, "fl_spec_verify: args is NULL");
+  if (a->struct_size != sizeof(fl_spec_args)) return fail(FL_EINVAL, "fl_spec_verify: struct_size mismatch");
+  if (a->dtype != FL_DTYPE_F32 && a->dtype != FL_DTYPE_BF16 && a->dtype != FL_DTYPE_F16)
+    return fail(FL_EINVAL, "fl_spec_verify: unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->k < 1 || a->vocab < 1 || a->ld < a->vocab)
+    return fail(FL_EINVAL, "fl_spec_verify: bad shape batch=%lld k=%lld vocab=%lld ld=%lld",
+                static_cast<long long>(a->batch), static_cast<long long>(a->k), static_cast<long long>(a->vocab),
+                static_cast<long long>(a->ld));
+  if (a->batch == 0) return ok();
+  if (!a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
+      !a->u_resample || !a->bonus_token || !a->out_n_accepted || !a->out_tokens)
+    return fail(FL_EINVAL, "fl_spec_verify: a required pointer is NULL");
+  const hipError_t e = fl::launch_spec_verify(*a, static_cast<hipStream_t>(stream));
+  return check_launch(e, "fl_spec_verify");
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// Device-side helpers shared by the sampling kernels (gfx950, wave64).
+//
+// Rounding helpers reproduce how PyTorch evaluates a reduced-precision tensor
+// op with a Python scalar operand: the element is widened to float32, combined
+// with the scalar rounded to float32, and the float32 result is rounded to the
+// tensor dtype with round-to-nearest-even.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fl_sampler.h"
+
+namespace fl {
+
+constexpr int NT = 1024;          // threads per work-group
+constexpr int WAVE = 64;
+constexpr int NWAVE = NT / WAVE;
+
+// ---------------------------------------------------------------- dtypes
+
+struct BF16 {
+  static constexpr int id = FL_DTYPE_BF16;
+  static constexpr uint32_t INF_BITS = 0x7F80u;
+  __device__ static __forceinline__ float to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+  __device__ static __forceinline__ uint32_t from_f32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // keep NaN a quiet NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  }
+  __device__ static __forceinline__ float rn(float x) { return to_f32(from_f32(x)); }
+};
+
+struct F16 {
+  static constexpr int id = FL_DTYPE_F16;
+  static constexpr uint32_t INF_BITS = 0x7C00u;
+  __device__ static __forceinline__ float to_f32(uint32_t b) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(b)));
+  }
+  __device__ static __forceinline__ uint32_t from_f32(float x) { return __half_as_ushort(__float2half_rn(x)); }
+  __device__ static __forceinline__ float rn(float x) { return to_f32(from_f32(x)); }
+};
+
+struct F32 {
+  static constexpr int id = FL_DTYPE_F32;
+  __device__ static __forceinline__ float rn(float x) { return x; }
+};
+
+// Order index of a 16-bit float pattern: 0 for the largest value (+NaN
+// patterns first), increasing towards the most negative value.
+__device__ __forceinline__ uint32_t order16(uint32_t bits) { return (bits & 0x8000u) ? bits : (0x7FFFu - bits); }
+__device__ __forceinline__ uint32_t bits_of_order16(uint32_t o) { return (o & 0x8000u) ? o : (0x7FFFu - o); }
+
+// Monotone uint32 key of a float32: larger float -> larger key.
+__device__ __forceinline__ uint32_t f32_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float f32_of_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// ------------------------------------------------- per-value transforms
+// Each mirrors one tensor op of the reference, evaluated in dtype D.
+
+// soft-cap tanh(x / c) * c  (models/attention/causal.py:109-110): three ops.
+template <class D>
+__device__ __forceinline__ float softcap_val(float x, float cap) {
+  const float a = D::rn(x / cap);
+  const float t = D::rn(tanhf(a));
+  return D::rn(t * cap);
+}
+
+// repetition penalty on one value (sampling.py:30): x>0 ? x/rp : x*rp.
+template <class D>
+__device__ __forceinline__ float penalty_val(float x, float rp) {
+  return x > 0.0f ? D::rn(x / rp) : D::rn(x * rp);
+}
+
+// temperature (sampling.py:33-34).
+template <class D>
+__device__ __forceinline__ float temperature_val(float x, float t) {
+  return t > 0.0f ? D::rn(x / t) : x;
+}
+
+// ------------------------------------------------- fixed-point masses
+// Probabilities in [0, 1] as unsigned 2^-46 fixed point: sums are exact and
+// associative (deterministic scans), and stay below 2^53 so that converting a
+// sum back to double is exact.
+constexpr double FX_ONE = 70368744177664.0;  // 2^46
+__device__ __forceinline__ uint64_t to_fx(float p) { return __double2ull_rn(static_cast<double>(p) * FX_ONE); }
+__device__ __forceinline__ double from_fx(uint64_t v) { return static_cast<double>(v) * (1.0 / FX_ONE); }
+
+// ------------------------------------------------------ reductions
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, WAVE); }
+template <typename T>
+__device__ __forceinline__ T shfl_up(T v, int d) { return __shfl_up(v, d, WAVE); }
+
+struct OpAdd { template <typename T> __device__ T operator()(T a, T b) const { return a + b; } };
+struct OpMin { template <typename T> __device__ T operator()(T a, T b) const { return b < a ? b : a; } };
+struct OpMax { template <typename T> __device__ T operator()(T a, T b) const { return a < b ? b : a; } };
+
+template <typename T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = op(v, shfl_xor(v, m));
+  return v;
+}
+
+// Block-wide reduction in a fixed order (deterministic for floating point).
+// `red` holds NWAVE elements of T.  Contains two barriers.
+template <typename T, class Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T* red) {
+  v = wave_reduce(v, op);
+  if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
+  __syncthreads();
+  T r = red[0];
+#pragma unroll
+  for (int i = 1; i < NWAVE; ++i) r = op(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+// Block-wide exclusive prefix sum in thread order; *total receives the sum.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int w = threadIdx.x / WAVE;
+  T inc = v;
+#pragma unroll
+  for (int d = 1; d < WAVE; d <<= 1) {
+    T t = shfl_up(inc, d);
+    if (lane >= d) inc = inc + t;
+  }
+  T exc = shfl_up(inc, 1);
+  if (lane == 0) exc = T(0);
+  if (lane == WAVE - 1) red[w] = inc;
+  __syncthreads();
+  T base = T(0), tot = T(0);
+#pragma unroll
+  for (int i = 0; i < NWAVE; ++i) {
+    const T x = red[i];
+    if (i < w) base = base + x;
+    tot = tot + x;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + exc;
+}
+
+// Indices held by this thread for a slice partition of n items.
+__device__ __forceinline__ void thread_slice(int n, int& lo, int& hi) {
+  const int per = (n + NT - 1) / NT;
+  lo = min(n, static_cast<int>(threadIdx.x) * per);
+  hi = min(n, lo + per);
+}
+
+// Membership of `tok` in row b's stop set.
+__device__ __forceinline__ bool is_stop(const int32_t* stop_ids, int64_t stop_ld, int64_t n_stop, int64_t b,
+                                        int64_t tok) {
+  if (stop_ids == nullptr || tok < 0) return false;
+  const int32_t* s = stop_ids + b * stop_ld;
+  for (int64_t i = 0; i < n_stop; ++i)
+    if (s[i] >= 0 && s[i] == tok) return true;
+  return false;
+}
+
+}  // namespace fl

@@ -1,0 +1,21 @@
+// Host-side launchers of the sampling kernels (one translation unit each).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/fl_sampler.h"
+
+namespace fl {
+
+// Row samplers: one work-group per row; a.dtype selects the kernel family.
+hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s);
+hipError_t launch_sample_rows32(const fl_sample_args& a, hipStream_t s);
+
+// Element-wise materialisation of filtered logits / probabilities / masks.
+hipError_t launch_apply_filter(const fl_sample_args& a, const fl_row_desc* desc, void* out_filtered, int64_t out_ld,
+                               float* out_probs, uint32_t* out_mask, hipStream_t s);
+
+// Speculative accept / residual resample, one work-group per sequence.
+hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s);
+
+}  // namespace fl
