@@ -1,0 +1,171 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X token-sampling path on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+One step = one fused sampling launch over one batch of synthetic logits
+already resident in HBM (default workload: B=256 rows, V=128256 bf16 logits,
+heterogeneous per-row temperature / top-k / top-p / min-p / repetition penalty
+over 2048 history ids).  Several distinct input batches (> 256 MB together)
+are rotated so that the 256 MB Infinity Cache cannot serve a repeated batch.
+
+Prints one JSON line: rows/s (= sampled tokens/s) over exactly K timed steps
+bracketed by device synchronisations, the dominant kernel's roofline (its
+average launch duration from HIP events on the launch stream, against the
+algorithmic bytes of one launch and MI355X's 8 TB/s HBM peak), and the CPU
+baseline (the oracle's per-row restatement of the reference sampler, timed on
+this host on a bounded sample of the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/sec at B=256,V=128256 mixed params; achieved HBM GB/s vs peak"
+DEFAULT_WORKLOAD = "hetero_bf16_256x128256"
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def _traffic_from_profile(workload: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), as recorded under profiles/."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(w, seconds: float):
+    """The oracle's per-row restatement (one [1, V] call per row, as the
+    reference inference engine makes them) on the first rows of the workload,
+    until ``seconds`` of CPU time have been spent."""
+    import torch
+
+    from oracle import sampler_oracle as O
+
+    def row_params(w, b):
+        hist = [] if w.history is None else [int(v) for v in w.history[b].tolist() if v >= 0]
+        stops = [] if w.stop_ids is None else [int(v) for v in w.stop_ids.tolist()]
+        return O.RowParams(float(w.temperature[b]), int(w.top_k[b]), float(w.top_p[b]), float(w.min_p[b]),
+                           float(w.repetition_penalty[b]), hist, stops)
+
+    x = w.logits.cpu()
+    u = w.uniforms.cpu().tolist()
+    rows = 0
+    t0 = time.perf_counter()
+    # one warm-up row
+    O.sample_rows(x[:1], [row_params(w, 0)], u[:1], softcap=w.softcap, want_filtered=False)
+    t0 = time.perf_counter()
+    while rows < w.batch and time.perf_counter() - t0 < seconds:
+        O.sample_rows(x[rows:rows + 1], [row_params(w, rows)], u[rows:rows + 1], softcap=w.softcap,
+                      want_filtered=False)
+        rows += 1
+    dt = time.perf_counter() - t0
+    return {"value": rows / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"rows 0..{rows - 1} of {w.name} (seed 0), one [1,V] oracle call per row "
+                      f"(torch {torch.__version__} CPU, {torch.get_num_threads()} threads, "
+                      f"{torch.backends.cpu.get_cpu_capability()}), {dt:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD)
+    ap.add_argument("--buffers", type=int, default=0, help="distinct input batches (default: > 256 MB in total)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: rows of a sampling batch are independent, so the path shards by "
+              f"rows with no communication; --gpus {args.gpus} (WORLD_SIZE={world}) is not run.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from rl_project_amd import workloads
+    from rl_project_amd.sampling import SamplerPlan
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    w = workloads.make(args.workload, seed=0)
+    batch_bytes = w.logits.numel() * w.logits.element_size()
+    nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))
+    wd = w.to(dev)
+    bufs = [wd.logits]
+    for s in range(1, nbuf):
+        bufs.append(workloads.make(args.workload, seed=s).logits.to(dev))
+    kw = wd.kwargs()
+    plans = [SamplerPlan(buf, **kw) for buf in bufs]
+    stream = torch.cuda.current_stream(dev)
+
+    for i in range(args.warmup):
+        plans[i % nbuf].launch()
+    torch.cuda.synchronize(dev)
+    status = plans[0].output.status
+    if int((status != 0).sum()):
+        print(f"rows failed: status {status.tolist()[:16]}", file=sys.stderr)
+        return 1
+
+    K = args.steps
+    ev_s = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ev_e = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for k in range(K):
+        ev_s[k].record(stream)
+        plans[k % nbuf].launch()
+        ev_e[k].record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    durs = sorted(s.elapsed_time(e) for s, e in zip(ev_s, ev_e))
+    kern_ms = sum(durs) / len(durs)
+
+    B = w.batch
+    alg_bytes = w.algorithmic_bytes()
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    ms_per_step = wall * 1e3 / K
+    result = {
+        "metric": METRIC,
+        "value": B * K / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w.logits.dtype],
+        "data": "synthetic",
+        "config": {"workload": w.name, "batch": B, "vocab": w.vocab,
+                   "history": 0 if w.history is None else int(w.history.size(1)),
+                   "input_buffers": nbuf, "tokens_per_s": B * K / wall},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
+                     "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
+                     "kernel_ms_p10": durs[len(durs) // 10], "kernel_ms_p90": durs[(9 * len(durs)) // 10],
+                     "kernel": "k_sample_rows16<BF16>" if w.logits.element_size() == 2 else "k_sample_rows32"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

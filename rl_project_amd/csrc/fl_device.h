@@ -10,7 +10,27 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <rocprim/warp/warp_reduce.hpp>
+#include <rocprim/warp/warp_scan.hpp>
+
 #include "../../include/fl_sampler.h"
+
+// Phase timestamps for kernel tuning builds (-DFL_PHASE_TIMES): thread 0 of
+// work-groups 0..3 records the constant-rate wall clock at each FL_MARK.
+#ifdef FL_PHASE_TIMES
+static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64];
+#define FL_MARK(n)                                                              \
+  do {                                                                          \
+    if (blockIdx.x < 4 && threadIdx.x == 0) {                                   \
+      fl_phase_ts[blockIdx.x * 16 + (n)] = wall_clock64();                      \
+      fl_phase_ts[64 + blockIdx.x * 16 + (n)] = clock64();                      \
+    }                                                                           \
+  } while (0)
+#else
+#define FL_MARK(n) \
+  do {             \
+  } while (0)
+#endif
 
 namespace fl {
 
@@ -46,6 +66,18 @@ struct F32 {
   static constexpr int id = FL_DTYPE_F32;
   __device__ static __forceinline__ float rn(float x) { return x; }
 };
+
+// Raw buffer access to one row: the hardware range check returns zeros for
+// bytes at or beyond `bytes`, so loads need neither clamped addresses nor
+// branches, and an address is one 32-bit offset (plus an SGPR offset).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // Order index of a 16-bit float pattern: 0 for the largest value (+NaN
 // patterns first), increasing towards the most negative value.
@@ -92,6 +124,13 @@ constexpr double FX_ONE = 70368744177664.0;  // 2^46
 __device__ __forceinline__ uint64_t to_fx(float p) { return __double2ull_rn(static_cast<double>(p) * FX_ONE); }
 __device__ __forceinline__ double from_fx(uint64_t v) { return static_cast<double>(v) * (1.0 / FX_ONE); }
 
+// Work-group barrier that orders LDS only: waits for this wave's LDS
+// operations (lgkmcnt) but not for its outstanding global loads (vmcnt), so
+// loads issued before it stay in flight.  __syncthreads() would drain them.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ------------------------------------------------------ reductions
 
 template <typename T>
@@ -103,11 +142,24 @@ struct OpAdd { template <typename T> __device__ T operator()(T a, T b) const { r
 struct OpMin { template <typename T> __device__ T operator()(T a, T b) const { return b < a ? b : a; } };
 struct OpMax { template <typename T> __device__ T operator()(T a, T b) const { return a < b ? b : a; } };
 
+// Wave-level reduction / scan through rocPRIM's cross-lane (DPP) primitives;
+// the combination order is fixed, so floating-point results are deterministic.
 template <typename T, class Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = op(v, shfl_xor(v, m));
-  return v;
+  using WR = rocprim::warp_reduce<T, WAVE, true>;
+  typename WR::storage_type st;
+  T out;
+  WR().reduce(v, out, st, op);
+  return out;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  using WS = rocprim::warp_scan<T, WAVE>;
+  typename WS::storage_type st;
+  T out;
+  WS().inclusive_scan(v, out, st, OpAdd());
+  return out;
 }
 
 // Block-wide reduction in a fixed order (deterministic for floating point).
@@ -129,12 +181,7 @@ template <typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int w = threadIdx.x / WAVE;
-  T inc = v;
-#pragma unroll
-  for (int d = 1; d < WAVE; d <<= 1) {
-    T t = shfl_up(inc, d);
-    if (lane >= d) inc = inc + t;
-  }
+  const T inc = wave_incl_scan(v);
   T exc = shfl_up(inc, 1);
   if (lane == 0) exc = T(0);
   if (lane == WAVE - 1) red[w] = inc;

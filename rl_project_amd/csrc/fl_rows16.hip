@@ -31,9 +31,11 @@ constexpr int NCH = 16;                          // 16-byte chunks per thread
 constexpr int HIST_WORDS = 32768;                // 65536 packed u16 counters
 constexpr int HBITS_WORDS = FL_MAX_VOCAB_16 / 32;
 constexpr int OWNER_WORDS = FL_MAX_HISTORY / 32;
-constexpr int LIST_CAP = HIST_WORDS / 2;         // candidates per identification target
+constexpr int LIST_CAP = 3 * HIST_WORDS / 8;     // candidates per identification target
+constexpr int HIT_CAP = HIST_WORDS / 4;          // queued chunks with a candidate (after the two lists)
 constexpr int ENTRY_CACHE_MAX = HIST_WORDS / 3;  // entries whose y and e fit beside the list
 constexpr int RANK_SELECT_MAX = 2048;            // candidates ranked by all-pairs counting
+constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 
 static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
 
@@ -44,6 +46,7 @@ struct Shared16 {
   double redd[NWAVE];
   uint64_t redq[NWAVE];
   uint32_t redu[NWAVE];
+  uint32_t redi_u[NWAVE];
   int32_t redi[NWAVE];
   int32_t status;
   int32_t n_entries;
@@ -54,7 +57,10 @@ struct Shared16 {
   uint64_t sel_cexcl;
   int32_t result[2];
   uint32_t nlist[2];
+  uint32_t nhit;
 };
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // 16-byte chunk c (elements 8c .. 8c+7) of a row; elements >= V read as 0.
 __device__ __forceinline__ uint4 load_chunk16(const uint16_t* row, int c, int V, bool aligned) {
@@ -76,57 +82,108 @@ __device__ __forceinline__ uint4 load_chunk16(const uint16_t* row, int c, int V,
 template <class D>
 __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM) {
   __shared__ Shared16 sh;
+  FL_MARK(0);
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int V = static_cast<int>(a.vocab);
   const uint16_t* row = static_cast<const uint16_t*>(a.logits) + b * a.ld;
+  const int nfull = V >> 3;                               // chunks holding 8 valid elements
+  const bool fast = ALIGNED && !SC_ELEM && nfull > 0;     // whole row through the VGPR tile
 
-  const float T = a.temperature ? a.temperature[b] : 1.0f;
-  const int K = a.top_k ? a.top_k[b] : 0;
-  const float TP = a.top_p ? a.top_p[b] : 1.0f;
-  const float MP = a.min_p ? a.min_p[b] : 0.0f;
-  const float RP = a.rep_penalty ? a.rep_penalty[b] : 1.0f;
+  // ------------------------------------------------ loads
+  // Issue order matters: the per-row parameters (scalar loads) first, so they
+  // do not queue behind 256 KB of row data; then the history ids (prefetched
+  // by row stride); then the row, branch-free with clamped addresses, so that
+  // waiting for the ids never waits for the row and all loads are in flight
+  // together.  The temperature array, always present, stands in for absent
+  // arrays so that every load is an unconditional global load.
+  const int32_t* dummy = reinterpret_cast<const int32_t*>(a.temperature);
+  const bool select = (a.flags & FL_FLAG_NO_SELECT) == 0;
+  const float T = a.temperature[b];
+  const int K = a.top_k[b];
+  const float TP = a.top_p[b];
+  const float MP = a.min_p[b];
+  const float RP = a.rep_penalty[b];
+  const float U_in = (select ? a.uniforms : a.temperature)[b];
+  const int H_in = (a.hist_ids ? a.hist_len : dummy)[b];
+  __builtin_amdgcn_sched_barrier(0);
+  const bool hist_rows = a.hist_ids != nullptr && a.hist_ld > 0;   // one id list per row
+  const int32_t* hid = a.hist_ids ? a.hist_ids + b * a.hist_ld : dummy;
+  const int32_t* hpre_src = hist_rows ? hid : dummy;
+  int32_t hpre[HPRE];
+#pragma unroll
+  for (int k = 0; k < HPRE; ++k) {
+    const int i = tid + k * NT;
+    hpre[k] = hpre_src[hist_rows ? min(i, static_cast<int>(a.hist_ld) - 1) : 0];
+  }
+  // ------------------------------------------------ clear LDS
+  // Before the row loads: a wave stalls in issuing its loads until the memory
+  // system accepts them (at the HBM rate), so a barrier placed after them
+  // would only open once the whole row had arrived.  Straight-line stores: a
+  // loop here makes the compiler wait for outstanding loads.
+  FL_MARK(10);
+  static_assert(HIST_WORDS == 8 * 4 * NT && HBITS_WORDS == 4 * NT && OWNER_WORDS <= 4 * NT, "LDS clear layout");
+#pragma unroll
+  for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(sh.hist)[tid + k * NT] = make_uint4(0, 0, 0, 0);
+  reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
+  if (tid < OWNER_WORDS / 4) reinterpret_cast<uint4*>(sh.owner)[tid] = make_uint4(0, 0, 0, 0);
+  if (tid == 0) {
+    sh.status = 0;
+    sh.nlist[0] = sh.nlist[1] = 0;
+    sh.nhit = 0;
+    sh.result[0] = sh.result[1] = -1;
+    sh.ik = 0;
+    sh.lk = 0;
+  }
+  lds_barrier();
+  FL_MARK(1);
+
+  // ------------------------------------------------ row loads (VGPR tile)
+  // (unconditional: behind a branch, the compiler's wait for the history ids
+  // would also wait for the row on the path that loaded it; a row the fast
+  // path does not take gets an empty range, so its loads return zeros)
+  const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast ? 2u * static_cast<uint32_t>(V) : 0u);
+  uint4 d[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+
   // u outside [0, 1) (or NaN) is clamped into it
-  const float U = fminf(fmaxf(a.uniforms ? a.uniforms[b] : 0.0f, 0.0f), 0.99999994f);
+  const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const float CAP = a.softcap;
-  const int H_in = (a.hist_ids != nullptr && a.hist_len != nullptr && RP != 1.0f) ? a.hist_len[b] : 0;
   const bool hist_too_long = H_in > FL_MAX_HISTORY;
-  const int H = hist_too_long ? 0 : H_in;
+  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
   const bool sc_entry = (CAP > 0.0f) && !SC_ELEM;
-  const bool select = (a.flags & FL_FLAG_NO_SELECT) == 0;
+  if (tid == 0 && hist_too_long) atomicOr(&sh.status, FL_ROW_LIMIT);
 
   // Value pattern of an element as the filters see it before penalty.
   auto elem_bits = [&](uint32_t raw) -> uint32_t {
     return SC_ELEM ? D::from_f32(softcap_val<D>(D::to_f32(raw), CAP)) : raw;
   };
-  const int nfull = V >> 3;                 // chunks holding 8 valid elements
-  const bool fast = ALIGNED && !SC_ELEM;    // whole row through the VGPR tile
 
-  // ------------------------------------------------ load the row (VGPRs)
-  uint4 d[NCH];
-  if (fast) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = j * NT + tid;
-      d[j] = (c < nfull) ? reinterpret_cast<const uint4*>(row)[c] : make_uint4(0, 0, 0, 0);
+  // ------------------------------------------------ history: unique ids
+  // Each id's first claimant owns it and fetches its logit now, so that the
+  // load overlaps the counting pass below.
+  uint32_t xh[HPRE];
+  bool own[HPRE];
+  auto claim = [&](int i, int id) -> bool {
+    if (id < 0 || id >= V) {
+      atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
+      return false;
     }
+    const uint32_t bit = 1u << (id & 31);
+    if (atomicOr(&sh.hbits[id >> 5], bit) & bit) return false;  // a duplicate id
+    atomicOr(&sh.owner[i >> 5], 1u << (i & 31));
+    return true;
+  };
+#pragma unroll
+  for (int k = 0; k < HPRE; ++k) {
+    const int i = tid + k * NT;
+    own[k] = pen && hist_rows && i < H;
+    if (own[k]) own[k] = claim(i, hpre[k]);
   }
-
-  // ------------------------------------------------ clear LDS
-  for (int i = tid; i < HIST_WORDS / 4; i += NT) reinterpret_cast<uint4*>(sh.hist)[i] = make_uint4(0, 0, 0, 0);
-  if (pen) {
-    for (int i = tid; i < (V + 31) / 32; i += NT) sh.hbits[i] = 0;
-    for (int i = tid; i < (H + 31) / 32; i += NT) sh.owner[i] = 0;
-  }
-  if (tid == 0) {
-    sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
-    sh.nlist[0] = sh.nlist[1] = 0;
-    sh.result[0] = sh.result[1] = -1;
-    sh.ik = 0;
-    sh.lk = 0;
-  }
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
 
   // ------------------------------------------------ count patterns
   auto count = [&](uint32_t bits) { atomicAdd(&sh.hist[bits >> 1], (bits & 1u) ? 0x10000u : 1u); };
@@ -150,64 +207,108 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   if (tid == 0)
     for (int i = nfull * 8; i < V; ++i) count(elem_bits(row[i]));
 
+  FL_MARK(12);
   // ------------------------------------------------ repetition penalty
-  const int32_t* hid = pen ? a.hist_ids + b * a.hist_ld : nullptr;
-  if (pen) {
-    for (int i = tid; i < H; i += NT) {
-      const int id = hid[i];
-      if (id < 0 || id >= V) {
-        atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
-        continue;
-      }
-      const uint32_t bit = 1u << (id & 31);
-      if (atomicOr(&sh.hbits[id >> 5], bit) & bit) continue;  // a duplicate id
-      atomicOr(&sh.owner[i >> 5], 1u << (i & 31));
-      const uint32_t z = elem_bits(row[id]);
-      const uint32_t zp = D::from_f32(penalty_val<D>(D::to_f32(z), RP));
-      if (zp != z) {
-        atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
-        atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
-      }
+  // each unique id moves one count from its pattern to its penalised pattern
+  auto penalise = [&](uint32_t raw) {
+    const uint32_t z = elem_bits(raw);
+    const uint32_t zp = D::from_f32(penalty_val<D>(D::to_f32(z), RP));
+    if (zp != z) {
+      atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
+      atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
     }
+  };
+#pragma unroll
+  for (int k = 0; k < HPRE; ++k)
+    if (own[k]) penalise(xh[k]);
+  for (int i = tid + (hist_rows ? HPRE * NT : 0); i < H; i += NT) {
+    const int id = hid[i];
+    if (claim(i, id)) penalise(row[id]);
   }
   __syncthreads();
+  FL_MARK(2);
 
   // ------------------------------------------------ compact to entries
-  // Thread t owns order indices [64t, 64t+64): threads < 512 the positive
-  // patterns (descending bits), the rest the negative ones (ascending bits).
+  // Wave w owns order indices [4096w, 4096w+4096): waves 0-7 the positive
+  // patterns (descending bits), 8-15 the negative ones (ascending bits).  Lane
+  // l reads word 64i+l of its wave's range in step i, so the 64 lanes of a
+  // read hit consecutive LDS words (no bank conflicts); a word's two
+  // counters are two consecutive order indices.  Positions come from ballots:
+  // entries are written in ascending order index.
   {
-    uint32_t w[32];
-    const bool pos = tid < NT / 2;
-    const int base_w = pos ? (0x3FE0 - 32 * tid) : (32 * tid);
+    const int wave = tid / WAVE;
+    const int lane = tid & (WAVE - 1);
+    const bool pos = wave < NWAVE / 2;  // wave-uniform
+    uint32_t x[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) w[i] = sh.hist[base_w + i];
-    auto cnt_at = [&](int q) -> uint32_t {
-      const uint32_t word = pos ? w[31 - (q >> 1)] : w[q >> 1];
-      return pos ? ((q & 1) ? (word & 0xFFFFu) : (word >> 16)) : ((q & 1) ? (word >> 16) : (word & 0xFFFFu));
+    for (int i = 0; i < 32; ++i) {
+      const int W = pos ? (0x3FFF - 2048 * wave - (64 * i + lane)) : (2048 * wave + 64 * i + lane);
+      x[i] = sh.hist[W];
+    }
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) any |= x[i];
+    const bool populated = __ballot(any != 0) != 0;  // wave-uniform
+    // halves in ascending order index: positive words hi then lo, negative lo then hi
+    auto first = [&](uint32_t w) { return pos ? (w >> 16) : (w & 0xFFFFu); };
+    auto second = [&](uint32_t w) { return pos ? (w & 0xFFFFu) : (w >> 16); };
+    auto word_of = [&](int i) { return pos ? (0x3FFF - 2048 * wave - (64 * i + lane)) : (2048 * wave + 64 * i + lane); };
+    // bits of the first / second half of word W
+    auto bits1 = [&](int W) { return pos ? 2u * W + 1 : 2u * W; };
+    auto bits2 = [&](int W) { return pos ? 2u * W : 2u * W + 1; };
+    const bool nan_range = wave == 0 || wave == NWAVE - 1;  // all NaN patterns live here
+    auto valid = [&](uint32_t cnt, uint32_t bits) {
+      return cnt != 0 && (!nan_range || (bits & 0x7FFFu) <= D::INF_BITS);
     };
-    uint32_t n_local = 0, sum_local = 0;
-    int32_t flags = 0;
+    uint32_t wtot = 0, lsum = 0;
+    bool nan = false;
+    if (populated && !nan_range) {
+      // SWAR: bit 15 / bit 31 set iff the low / high counter is non-zero
+      uint32_t lcnt = 0;
 #pragma unroll
-    for (int q = 0; q < 64; ++q) {
-      const uint32_t cnt = cnt_at(q);
-      const uint32_t bits = bits_of_order16(64 * tid + q);
-      sum_local += cnt;
-      if (cnt) {
-        if ((bits & 0x7FFFu) > D::INF_BITS) flags |= FL_ROW_NAN;
-        else ++n_local;
+      for (int i = 0; i < 32; ++i) {
+        lcnt += __popc((((x[i] & 0x7FFF7FFFu) + 0x7FFF7FFFu) | x[i]) & 0x80008000u);
+        lsum += (x[i] & 0xFFFFu) + (x[i] >> 16);
+      }
+      wtot = wave_reduce(lcnt, OpAdd());
+    } else if (populated) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int W = word_of(i);
+        const uint32_t a1 = first(x[i]), a2 = second(x[i]);
+        const bool v1 = valid(a1, bits1(W)), v2 = valid(a2, bits2(W));
+        nan |= (a1 != 0 && !v1) || (a2 != 0 && !v2);
+        wtot += __popcll(__ballot(v1)) + __popcll(__ballot(v2));
+        lsum += a1 + a2;
       }
     }
-    if (flags) atomicOr(&sh.status, flags);
-    uint32_t n_total;
-    uint32_t p = block_excl_scan<uint32_t>(n_local, sh.redu, &n_total);
-    const uint32_t total_cnt = block_reduce<uint32_t>(sum_local, OpAdd(), sh.redu);
+    if (nan) atomicOr(&sh.status, FL_ROW_NAN);
+    if (lane == 0) sh.redu[wave] = wtot;
+    const uint32_t total_cnt = block_reduce<uint32_t>(lsum, OpAdd(), sh.redi_u);  // includes a barrier
+    uint32_t base = 0, n_total = 0;
 #pragma unroll
-    for (int q = 0; q < 64; ++q) {
-      const uint32_t cnt = cnt_at(q);
-      const uint32_t bits = bits_of_order16(64 * tid + q);
-      if (cnt && (bits & 0x7FFFu) <= D::INF_BITS) {
-        if (p < static_cast<uint32_t>(HIST_WORDS)) sh.hist[p] = (static_cast<uint32_t>(64 * tid + q) << 16) | cnt;
-        ++p;
+    for (int i = 0; i < NWAVE; ++i) {
+      const uint32_t t = sh.redu[i];
+      if (i < wave) base += t;
+      n_total += t;
+    }
+    if (wtot) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (__ballot(x[i] != 0) == 0) continue;  // 64 empty words (wave-uniform)
+        const int W = word_of(i);
+        const uint32_t a1 = first(x[i]), a2 = second(x[i]);
+        const bool v1 = valid(a1, bits1(W)), v2 = valid(a2, bits2(W));
+        const uint64_t m1 = __ballot(v1), m2 = __ballot(v2);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0)) +
+                               __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
+        const uint32_t p1 = base + below;
+        if (v1 && p1 < static_cast<uint32_t>(HIST_WORDS)) sh.hist[p1] = (order16(bits1(W)) << 16) | a1;
+        const uint32_t p2 = p1 + (v1 ? 1u : 0u);
+        if (v2 && p2 < static_cast<uint32_t>(HIST_WORDS)) sh.hist[p2] = (order16(bits2(W)) << 16) | a2;
+        base += __popcll(m1) + __popcll(m2);
       }
     }
     if (tid == 0) {
@@ -218,6 +319,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
   }
   __syncthreads();
+  FL_MARK(3);
 
   const int N = sh.n_entries;
   uint32_t* ent = sh.hist;
@@ -253,6 +355,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
   }
   __syncthreads();
+  FL_MARK(4);
   auto Y = [&](int i) -> float { return cached ? Yc[i] : ent_y(i); };
   auto E = [&](int i) -> float { return cached ? Ec[i] : expf(ent_y(i) - M); };
 
@@ -463,6 +566,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const float y_sel = (status == 0 && select) ? Y(sel_lo) : 0.0f;
   const float y_cut = (status == 0) ? Y(i0) : __builtin_inff();
   __syncthreads();
+  FL_MARK(6);
 
   // ------------------------------------------------ identification
   // Targets: 0 = selected token (group sel, rank sel_rank); 1 = last kept
@@ -477,33 +581,102 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 
   if (active[0] || active[1]) {
     uint32_t* list[2] = {sh.hist, sh.hist + LIST_CAP};
+    uint32_t* hitq = sh.hist + 2 * LIST_CAP;
     auto in_range = [&](int t, uint32_t bits) { return order16(bits) - o_lo[t] <= o_hi[t] - o_lo[t]; };
     auto is_hist = [&](int idx) { return pen && ((sh.hbits[idx >> 5] >> (idx & 31)) & 1u); };
-    // non-history elements whose value lies in a target group (re-reads the row)
-    for (int c = tid; c < (V + 7) / 8; c += NT) {
-      const uint4 q = load_chunk16(row, c, V, ALIGNED);
+    // The targets' order ranges as at most four ranges of raw bit patterns
+    // (a range across zero splits into its positive and negative parts).
+    // (slots 2t, 2t+1 belong to target t; fixed slots keep the arrays in VGPRs)
+    // Range r covers patterns rlo[r] .. rlo[r] + rw[r].
+    uint32_t rlo[4] = {0, 0, 0, 0}, rw[4] = {0, 0, 0, 0};
+    bool ren[4] = {false, false, false, false};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (!active[t]) continue;
+      if (o_hi[t] < 0x8000u) {
+        rlo[2 * t] = 0x7FFFu - o_hi[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+      } else if (o_lo[t] >= 0x8000u) {
+        rlo[2 * t] = o_lo[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+      } else {
+        rlo[2 * t] = 0u, rw[2 * t] = 0x7FFFu - o_lo[t], ren[2 * t] = true;
+        rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
+      }
+    }
+    // Packed 16-bit range test of both halves of a word: a wrapping subtract
+    // of the range start, then a saturating subtract of the width, leaves 0
+    // exactly in the halves inside the range.
+    auto range_test = [&](uint32_t w, int r) -> uint32_t {
+      const u16x2 d = __builtin_bit_cast(u16x2, w) - u16x2{static_cast<unsigned short>(rlo[r]),
+                                                            static_cast<unsigned short>(rlo[r])};
+      return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(
+                                              d, u16x2{static_cast<unsigned short>(rw[r]),
+                                                       static_cast<unsigned short>(rw[r])}));
+    };
+    // non-zero iff a half of e is zero (may also flag a half above a zero
+    // one; the exact test on the hit path sorts that out)
+    auto zero_halves = [](uint32_t e) { return (e - 0x00010001u) & ~e & 0x80008000u; };
+    auto candidate = [&](int idx, int t) {
+      if (idx < V && !is_hist(idx)) {
+        const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
+        if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = idx;
+      }
+    };
+    // Element work for one chunk (patterns recomputed one by one).
+    auto chunk_candidates = [&](int c, const uint4 q) {
       const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int idx = c * 8 + e;
-        if (idx < V) {
-          const uint32_t bits = elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
+        const uint32_t bits = elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            if (active[t] && in_range(t, bits) && !is_hist(idx)) {
-              const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
-              if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = idx;
-            }
-          }
+        for (int t = 0; t < 2; ++t)
+          if (active[t] && in_range(t, bits)) candidate(c * 8 + e, t);
+      }
+    };
+    const int nchunks = (V + 7) >> 3;
+    if (fast) {
+      // Non-history elements whose value lies in a target group.  The row is
+      // read again, all chunks in flight at once (mostly a cache hit); each
+      // chunk gets a branch-free packed test, and the rare hit chunks are
+      // queued in LDS and examined element by element afterwards, which keeps
+      // this loop small enough to stay unrolled with the tile in VGPRs.
+      uint4 r[NCH];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) r[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+      FL_MARK(13);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        uint32_t any = 0;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if (!ren[rr]) continue;  // wave-uniform
+          any |= zero_halves(range_test(r[j].x, rr)) | zero_halves(range_test(r[j].y, rr)) |
+                 zero_halves(range_test(r[j].z, rr)) | zero_halves(range_test(r[j].w, rr));
+        }
+        const int c = j * NT + tid;
+        if (any != 0 && c < nchunks) {
+          const uint32_t s = atomicAdd(&sh.nhit, 1u);
+          if (s < static_cast<uint32_t>(HIT_CAP)) hitq[s] = c;
         }
       }
+      FL_MARK(14);
+      __syncthreads();
+      const uint32_t nhit = sh.nhit;
+      if (nhit <= static_cast<uint32_t>(HIT_CAP)) {
+        for (int i = tid; i < static_cast<int>(nhit); i += NT) {
+          const int c = hitq[i];
+          chunk_candidates(c, buf_load16(rrow, 16u * c, 0u));
+        }
+      } else {
+        for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, buf_load16(rrow, 16u * c, 0u));
+      }
+    } else {
+      for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, load_chunk16(row, c, V, ALIGNED));
     }
-    // history elements whose penalised value lies in a target group
+    // history elements whose penalised value lies in a target group (the
+    // first HPRE ids of each thread and their logits are still in registers)
     if (pen) {
-      for (int i = tid; i < H; i += NT) {
-        if (!((sh.owner[i >> 5] >> (i & 31)) & 1u)) continue;
-        const int id = hid[i];
-        const uint32_t z = elem_bits(row[id]);
+      auto hist_candidate = [&](int id, uint32_t raw) {
+        const uint32_t z = elem_bits(raw);
         const uint32_t zp = D::from_f32(penalty_val<D>(D::to_f32(z), RP));
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -512,9 +685,18 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
             if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = id;
           }
         }
+      };
+#pragma unroll
+      for (int k = 0; k < HPRE; ++k)
+        if (own[k]) hist_candidate(hpre[k], xh[k]);
+      for (int i = tid + (hist_rows ? HPRE * NT : 0); i < H; i += NT) {
+        if (!((sh.owner[i >> 5] >> (i & 31)) & 1u)) continue;
+        const int id = hid[i];
+        hist_candidate(id, row[id]);
       }
     }
     __syncthreads();
+    FL_MARK(7);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
@@ -560,8 +742,10 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
   }
   __syncthreads();
+  FL_MARK(8);
 
   // ------------------------------------------------ outputs
+  FL_MARK(9);
   if (tid == 0) {
     int64_t tok = -1;
     if (want_sel) {
@@ -613,3 +797,11 @@ hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s) {
 }
 
 }  // namespace fl
+
+#ifdef FL_PHASE_TIMES
+// Tuning builds only: copy the phase timestamps recorded by the last launch.
+extern "C" int fl_debug_phase_ts(uint64_t* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * 192, 0, hipMemcpyDeviceToHost) ==
+                 hipSuccess ? 0 : -1;
+}
+#endif

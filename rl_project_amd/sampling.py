@@ -171,6 +171,32 @@ class _Call:
         return self
 
 
+class SamplerPlan:
+    """A prepared ``sample_tokens`` call: arguments and output buffers are
+    built once, each ``launch()`` only enqueues the kernel (no allocation, no
+    host synchronisation) -- for decode loops that resample the same buffers.
+    Reads ``logits`` and the parameter tensors at launch time, so callers may
+    overwrite them in place between launches."""
+
+    def __init__(self, logits: torch.Tensor, **kw):
+        want_logprob = kw.pop("return_logprobs", False)
+        want_desc = kw.pop("return_desc", False)
+        self._call = _Call(logits, flags=0, want_logprob=want_logprob, want_desc=want_desc,
+                           finished=kw.pop("finished", None), uniforms=kw.pop("uniforms", None), **kw)
+        self._fn = lib().fl_sample
+        self._argp = ctypes.byref(self._call.args)
+
+    def launch(self) -> None:
+        rc = self._fn(self._argp, self._call.stream)
+        if rc:
+            check(rc, "fl_sample")
+
+    @property
+    def output(self) -> SampleOutput:
+        c = self._call
+        return SampleOutput(c.tokens, c.finished.bool(), c.status, c.logprob, c.desc)
+
+
 def _raise_on_status(status: torch.Tensor, allowed: int = 0) -> None:
     bad = status & ~allowed
     if bool((bad != 0).any()):
