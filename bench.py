@@ -60,18 +60,18 @@ def cpu_baseline(w, seconds: float):
 
     x = w.logits.cpu()
     u = w.uniforms.cpu().tolist()
+    params = [row_params(w, b) for b in range(w.batch)]
+    # one warm-up row, then rows 0, 1, ... (cycling through the batch) until the time is spent
+    O.sample_rows(x[:1], params[:1], u[:1], softcap=w.softcap, want_filtered=False)
     rows = 0
     t0 = time.perf_counter()
-    # one warm-up row
-    O.sample_rows(x[:1], [row_params(w, 0)], u[:1], softcap=w.softcap, want_filtered=False)
-    t0 = time.perf_counter()
-    while rows < w.batch and time.perf_counter() - t0 < seconds:
-        O.sample_rows(x[rows:rows + 1], [row_params(w, rows)], u[rows:rows + 1], softcap=w.softcap,
-                      want_filtered=False)
+    while time.perf_counter() - t0 < seconds:
+        b = rows % w.batch
+        O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap, want_filtered=False)
         rows += 1
     dt = time.perf_counter() - t0
     return {"value": rows / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"rows 0..{rows - 1} of {w.name} (seed 0), one [1,V] oracle call per row "
+            "sample": f"{rows} rows of {w.name} (seed 0, cycling through its {w.batch} rows), one [1,V] oracle call per row "
                       f"(torch {torch.__version__} CPU, {torch.get_num_threads()} threads, "
                       f"{torch.backends.cpu.get_cpu_capability()}), {dt:.1f} s"}
 
@@ -85,6 +85,9 @@ def main() -> int:
     ap.add_argument("--buffers", type=int, default=0, help="distinct input batches (default: > 256 MB in total)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run an elementwise read+write kernel (torch.neg) over MIB MiB, 5 launches: the "
+                         "known-size kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -102,6 +105,15 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.arange(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"calibrate_copy_bytes": 4 * n, "launches": 5}), flush=True)
+        return 0
     w = workloads.make(args.workload, seed=0)
     batch_bytes = w.logits.numel() * w.logits.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))
