@@ -53,6 +53,10 @@ int validate_sample(const fl_sample_args* a, const char* fn) {
     return fail(FL_EINVAL, "%s: hist_ids needs hist_len and hist_ld >= 0", fn);
   if (a->n_stop < 0 || (a->n_stop > 0 && (a->stop_ids == nullptr || a->stop_ld < 0)))
     return fail(FL_EINVAL, "%s: stop_ids/n_stop/stop_ld inconsistent", fn);
+  if (a->batch > 0 && (a->temperature == nullptr || a->top_k == nullptr || a->top_p == nullptr ||
+                       a->min_p == nullptr || a->rep_penalty == nullptr))
+    return fail(FL_EINVAL, "%s: the per-row parameter arrays (temperature, top_k, top_p, min_p, rep_penalty) "
+                           "are required", fn);
   return FL_OK;
 }
 
@@ -69,6 +73,8 @@ int fl_sample(const fl_sample_args* a, void* stream) {
   if (rc != FL_OK) return rc;
   const bool select = (a->flags & FL_FLAG_NO_SELECT) == 0;
   if (select && a->out_token == nullptr) return fail(FL_EINVAL, "fl_sample: out_token is NULL");
+  if (select && a->batch > 0 && a->uniforms == nullptr)
+    return fail(FL_EINVAL, "fl_sample: uniforms is NULL (one draw per row is required unless FL_FLAG_NO_SELECT)");
   if (a->batch == 0) return ok();
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = a->dtype == FL_DTYPE_F32 ? fl::launch_sample_rows32(*a, s) : fl::launch_sample_rows16(*a, s);
@@ -81,6 +87,8 @@ int fl_apply_filter(const fl_sample_args* a, const fl_row_desc* desc, void* out_
   if (rc != FL_OK) return rc;
   if (desc == nullptr) return fail(FL_EINVAL, "fl_apply_filter: desc is NULL");
   if (out_filtered != nullptr && out_ld < a->vocab) return fail(FL_EINVAL, "fl_apply_filter: out_ld < vocab");
+  if (a->batch > 65535) return fail(FL_ENOTSUP, "fl_apply_filter: batch %lld exceeds 65535",
+                                    static_cast<long long>(a->batch));
   if (a->batch == 0 || (out_filtered == nullptr && out_probs == nullptr && out_mask == nullptr)) return ok();
   const hipError_t e =
       fl::launch_apply_filter(*a, desc, out_filtered, out_ld, out_probs, out_mask, static_cast<hipStream_t>(stream));

@@ -1,7 +1,770 @@
-// Fused per-row sampler for float32 logits (placeholder until the fp32 path lands).
+// Fused per-row sampler for float32 logits on gfx950.
+//
+// One work-group of 1024 threads owns one row.  Float32 rows have too many
+// distinct values to histogram exactly, so each decision of the reference
+// sampler (src/forgeline/models/generation/sampling.py:26-61) is located by
+// radix narrowing on an order-preserving 32-bit key of the filtered value y:
+//
+//   max      a pass over the row finds M = max y (the softmax shift) and
+//            checks for NaN / +inf
+//   bins     a pass builds 2048 bins on key bits 31..21; each bin holds its
+//            element count and its mass sum(exp(y - M)) in 2^-45 fixed point,
+//            so every partial sum is exact and order-independent
+//   narrow   the decision point (the k-th value, the min-p boundary, the top-p
+//            crossing, the inverse-CDF target) is located in one bin by a block
+//            scan over the bins; a bin with more than CAP elements is split on
+//            the next 11, then 10, key bits by another pass
+//   exact    the elements of the final bin are gathered into LDS as
+//            (key, index) pairs, sorted by descending value then ascending
+//            index, and the decision is made element by element.
+//
+// Float32 decisions use exact arithmetic on the fixed-point masses:
+//   top-k  keeps y >= the k-th largest value (ties kept)          (:36-38)
+//   min-p  keeps exp(y - M) >= min_p, the reference's p < min_p * max p with
+//          the common 1/S factor cancelled                          (:40-43)
+//   top-p  removes sorted position j when the mass before it reaches
+//          top_p times the mass of the survivors                    (:45-51)
+//   select inverse CDF: the first member, in descending value / ascending
+//          index order, whose inclusive mass exceeds u times the kept mass
+//          (replaces torch.multinomial, :61); T <= 0 takes the first index of
+//          the maximal value (argmax, :59-60).
+// The reference evaluates the same predicates through float32 softmax and
+// cumsum roundings; the two can differ only where a quantity lies within a few
+// ulp of its threshold.
+//
+// Every pass reads the row again: the first from HBM, later ones mostly from
+// L2 for rows of up to a few hundred KB.
+#include <climits>
+
 #include "fl_device.h"
 #include "fl_kernels.h"
 
 namespace fl {
-hipError_t launch_sample_rows32(const fl_sample_args&, hipStream_t) { return hipErrorNotSupported; }
+
+namespace {
+
+constexpr int NB = 2048;                   // bins of the first two narrowing levels
+constexpr int NB3 = 1024;                  // bins of the last level (one key each)
+constexpr int CAP = 4096;                  // elements gathered and sorted in LDS
+constexpr uint32_t KEY_POS_INF = 0xFF800000u;
+constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;
+constexpr uint32_t KEY_MIN_FINITE = 0x00800000u;  // smallest key of a value above -inf
+constexpr int FXB = 45;                    // 2^-45 fixed point: 2^18 unit terms fit in 64 bits
+
+// e in [0, 1] as fixed point round(e * 2^45) (halves rounded up).
+__device__ __forceinline__ uint64_t fx45(float e) {
+  const uint32_t u = __float_as_uint(e);
+  const int ex = static_cast<int>(u >> 23);
+  if (ex == 0) return 0;  // zero or denormal: below the resolution
+  const uint64_t m = (u & 0x7FFFFFu) | 0x800000u;  // e = m * 2^(ex - 150)
+  const int s = ex - 150 + FXB;
+  if (s >= 0) return m << s;
+  if (s < -24) return 0;
+  return (m + (1ull << (-s - 1))) >> (-s);
+}
+__device__ __forceinline__ double from_fx45(uint64_t v) { return static_cast<double>(v) * (1.0 / 35184372088832.0); }
+
+struct Shared32 {
+  uint32_t cnt1[NB];   // level-1 bins, kept for every decision
+  uint64_t mass1[NB];
+  uint32_t cnt[NB];    // deeper levels
+  uint64_t mass[NB];
+  uint64_t cand[CAP];  // (key << 32) | ~index, sorted descending
+  uint64_t redq[NWAVE];
+  uint32_t redu[NWAVE];
+  int32_t redi[NWAVE];
+  int32_t status;
+  uint32_t ncand;
+  int32_t pick_bin;
+  uint32_t pick_n;
+  uint64_t pick_m;
+  int32_t result;
+  uint32_t bcast_u;
+  uint64_t bcast_q;
+};
+
+// Element source: raw buffer loads of one row (range-checked, so loads past
+// the row return zeros and need no clamping).
+struct Src {
+  __amdgpu_buffer_rsrc_t rs;
+  int V;
+  int nfull;  // chunks of 4 elements that lie wholly inside the row
+  bool aligned;
+  __device__ __forceinline__ float4 chunk(int c) const {
+    if (aligned && c < nfull) {
+      const uint4 u = buf_load16(rs, 16u * c, 0u);
+      return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    }
+    float4 f;
+    f.x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 16 * c + 0, 0, 0));
+    f.y = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 16 * c + 4, 0, 0));
+    f.z = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 16 * c + 8, 0, 0));
+    f.w = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 16 * c + 12, 0, 0));
+    return f;
+  }
+};
+
+// Logit -> filtered value: soft-cap, repetition penalty (history elements),
+// temperature, each rounded to float32 as the reference's tensor ops round.
+struct Xform {
+  float cap, rp, t;
+  bool pen;
+  const uint32_t* hbits;
+  int nch;
+  __device__ __forceinline__ float y(float x, bool hist) const {
+    float z = x;
+    if (cap > 0.0f) z = softcap_val<F32>(z, cap);
+    if (hist) z = penalty_val<F32>(z, rp);
+    // + 0.0f turns -0 into +0: the filters compare -0 == +0, so both get one key
+    return temperature_val<F32>(z, t) + 0.0f;
+  }
+  // history bits of elements 4c .. 4c+3
+  __device__ __forceinline__ uint32_t nibble(int c) const {
+    return (pen && c < nch) ? (hbits[c >> 3] >> ((c & 7) * 4)) & 0xFu : 0u;
+  }
+};
+
+// f(idx, y, valid) for every element of the row, read from memory: the first
+// pass streams the row from HBM, later passes of a row of up to a few hundred
+// KB mostly hit L2.  Called by all threads (block-uniform control flow).
+template <class F>
+__device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f) {
+  const int tid = threadIdx.x;
+  const int nch = X.nch;
+  for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * NT + tid;
+      const uint32_t hb = X.nibble(c);
+      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int idx = 4 * c + e;
+        f(idx, X.y(xs[e], (hb >> e) & 1u), idx < S.V);
+      }
+      // one chunk's elements at a time (interleaving all 16 costs VGPRs)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// Wave-aggregated append of v to buf (one LDS atomic per wave).
+__device__ __forceinline__ void wave_append(bool p, uint64_t v, uint32_t* counter, uint64_t* buf) {
+  const uint64_t m = __ballot(p);
+  if (m == 0) return;
+  const uint32_t below =
+      __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+  const int leader = __ffsll(static_cast<unsigned long long>(m)) - 1;
+  uint32_t base = 0;
+  if ((threadIdx.x & (WAVE - 1)) == leader) base = atomicAdd(counter, static_cast<uint32_t>(__popcll(m)));
+  base = __shfl(base, leader, WAVE);
+  if (p && base + below < static_cast<uint32_t>(CAP)) buf[base + below] = v;
+}
+
+// Descending bitonic sort of buf[0, n) in LDS (n <= CAP); pads with zeros.
+__device__ void bitonic_desc(uint64_t* buf, int n) {
+  int P = 2;
+  while (P < n) P <<= 1;
+  for (int i = n + threadIdx.x; i < P; i += NT) buf[i] = 0;
+  __syncthreads();
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (P >> 1); i += NT) {
+        const int a = 2 * j * (i / j) + (i % j);
+        const int c = a + j;
+        const uint64_t x = buf[a], y = buf[c];
+        const bool desc = (a & k) == 0;
+        if (desc ? (x < y) : (x > y)) {
+          buf[a] = y;
+          buf[c] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+enum Crit { CRIT_COUNT = 0, CRIT_PRED = 1, CRIT_MASS = 2 };
+
+// The bin holding a decision point, scanning bins in descending key order
+// with exact running totals.  Bins lying wholly below key `tau` are skipped
+// (their elements are already removed) except by CRIT_COUNT.
+//   CRIT_COUNT: first bin whose inclusive count exceeds `rank`
+//   CRIT_PRED : first bin whose smallest possible value fails exp(y - M) >= mp
+//   CRIT_MASS : first bin whose inclusive mass reaches `thr`
+struct Pick {
+  int bin;        // -1 when no bin qualifies
+  uint32_t n_ex;  // elements before the bin (whole row order)
+  uint64_t m_ex;  // their mass
+};
+
+__device__ Pick choose_bin(Shared32& sh, const uint32_t* cnt, const uint64_t* mass, int nbins, uint32_t klo, int shift,
+                           uint32_t n_ab, uint64_t m_ab, int crit, uint32_t rank, float mp, float M, uint64_t thr,
+                           uint32_t tau) {
+  const int per = (nbins + NT - 1) / NT;
+  const int p0 = threadIdx.x * per;
+  uint32_t ln = 0;
+  uint64_t lm = 0;
+  for (int k = 0; k < per; ++k) {
+    const int pos = p0 + k;
+    if (pos < nbins) {
+      ln += cnt[nbins - 1 - pos];
+      lm += mass[nbins - 1 - pos];
+    }
+  }
+  uint32_t tn;
+  uint64_t tm;
+  const uint32_t en = block_excl_scan<uint32_t>(ln, sh.redu, &tn);
+  const uint64_t em = block_excl_scan<uint64_t>(lm, sh.redq, &tm);
+  uint32_t cn = n_ab + en;
+  uint64_t cm = m_ab + em;
+  int first = INT_MAX;
+  uint32_t fn = 0;
+  uint64_t fm = 0;
+  for (int k = 0; k < per; ++k) {
+    const int pos = p0 + k;
+    if (pos >= nbins) break;
+    const int bin = nbins - 1 - pos;
+    const uint32_t c = cnt[bin];
+    const uint64_t m = mass[bin];
+    if (c > 0 && first == INT_MAX) {
+      const uint32_t lo = klo + (static_cast<uint32_t>(bin) << shift);
+      const uint32_t hi = lo + ((1u << shift) - 1u);
+      bool hit;
+      if (crit == CRIT_COUNT) hit = cn + c > rank;
+      else if (crit == CRIT_PRED) hit = hi >= tau && !(expf(f32_of_key(lo) - M) >= mp);
+      else hit = hi >= tau && cm + m >= thr;
+      if (hit) {
+        first = pos;
+        fn = cn;
+        fm = cm;
+      }
+    }
+    cn += c;
+    cm += m;
+  }
+  const int w = block_reduce<int32_t>(first, OpMin(), sh.redi);
+  if (w == INT_MAX) return {-1, 0, 0};
+  if (first == w) {
+    sh.pick_bin = nbins - 1 - w;
+    sh.pick_n = fn;
+    sh.pick_m = fm;
+  }
+  __syncthreads();
+  Pick p = {sh.pick_bin, sh.pick_n, sh.pick_m};
+  __syncthreads();
+  return p;
+}
+
+// Outcome of a narrowing
+enum Outcome {
+  OUT_NONE = 0,     // no bin qualifies: the decision point lies past the row
+  OUT_CAND = 1,     // candidates sorted in sh.cand[0, n)
+  OUT_VALUE = 2,    // a single key with more than CAP elements
+  OUT_ALLKEPT = 3,  // the qualifying range splits into bins none of which qualifies
+};
+struct Narrow {
+  int out;
+  uint32_t klo, khi;  // key range
+  uint32_t n_ab;      // elements before the range (whole-row order)
+  uint64_t m_ab;      // their mass
+  uint32_t count;     // elements in the range
+  uint64_t rmass;     // their mass
+  int n;              // candidates gathered (OUT_CAND)
+};
+
+}  // namespace
+
+__global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
+  __shared__ Shared32 sh;
+  extern __shared__ uint32_t hbits_dyn[];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int V = static_cast<int>(a.vocab);
+  const float* row = static_cast<const float*>(a.logits) + b * a.ld;
+  const bool select = (a.flags & FL_FLAG_NO_SELECT) == 0;
+
+  const float T = a.temperature[b];
+  const int K = a.top_k[b];
+  const float TP = a.top_p[b];
+  const float MP = a.min_p[b];
+  const float RP = a.rep_penalty[b];
+  const float U_in = select ? a.uniforms[b] : 0.0f;
+  const int H_in = a.hist_ids ? a.hist_len[b] : 0;
+  const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
+  const bool hist_too_long = H_in > FL_MAX_HISTORY;
+  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
+  const bool pen = H > 0;
+  const int nch = (V + 3) >> 2;
+
+  if (tid == 0) {
+    sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
+    sh.result = -1;
+  }
+  // ------------------------------------------------ history bitmap
+  if (pen) {
+    for (int i = tid; i < (V + 31) / 32; i += NT) hbits_dyn[i] = 0;
+  }
+  __syncthreads();
+  if (pen) {
+    const int32_t* hid = a.hist_ids + b * a.hist_ld;
+    for (int i = tid; i < H; i += NT) {
+      const int id = hid[i];
+      if (id < 0 || id >= V) atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
+      else atomicOr(&hbits_dyn[id >> 5], 1u << (id & 31));
+    }
+  }
+  __syncthreads();
+
+  Src S;
+  S.rs = row_rsrc(row, 4u * static_cast<uint32_t>(V));
+  S.V = V;
+  S.nfull = V >> 2;
+  S.aligned = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+  Xform X;
+  X.cap = a.softcap;
+  X.rp = RP;
+  X.t = T;
+  X.pen = pen;
+  X.hbits = hbits_dyn;
+  X.nch = nch;
+
+  // ------------------------------------------------ first read: max, NaN
+  uint32_t kmax = 0;
+  int nan = 0;
+  row_pass(S, X, [&](int, float y, bool valid) {
+    if (valid) {
+      if (y != y) nan = 1;
+      else kmax = max(kmax, f32_key(y));
+    }
+  });
+  kmax = block_reduce<uint32_t>(kmax, OpMax(), sh.redu);
+  nan = block_reduce<int32_t>(nan, OpMax(), sh.redi);
+  if (tid == 0) {
+    if (nan) sh.status |= FL_ROW_NAN;
+    else if (kmax >= KEY_POS_INF) sh.status |= FL_ROW_INF;
+    else if (kmax <= KEY_NEG_INF) sh.status |= FL_ROW_ALL_MASKED;
+  }
+  __syncthreads();
+  int32_t status = sh.status;
+  const float M = f32_of_key(kmax);
+
+  // ------------------------------------------------ helpers
+  auto hist_pass = [&](uint32_t* cnt, uint64_t* mass, uint32_t klo, int shift, int nb) __attribute__((always_inline)) {
+    for (int i = tid; i < nb; i += NT) {
+      cnt[i] = 0;
+      mass[i] = 0;
+    }
+    __syncthreads();
+    row_pass(S, X, [&](int, float y, bool valid) {
+      const uint32_t bin = (f32_key(y) - klo) >> shift;
+      if (valid && bin < static_cast<uint32_t>(nb)) {
+        atomicAdd(&cnt[bin], 1u);
+        const uint64_t f = fx45(expf(y - M));
+        if (f) atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(f));
+      }
+    });
+    __syncthreads();
+  };
+  auto collect = [&](uint32_t klo, uint32_t khi) -> int __attribute__((always_inline)) {
+    int n;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+    row_pass(S, X, [&](int idx, float y, bool valid) {
+      const uint32_t k = f32_key(y);
+      const bool in = valid && (k - klo) <= (khi - klo);
+      wave_append(in, (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(idx)),
+                  &sh.ncand, sh.cand);
+    });
+    __syncthreads();
+    n = min(static_cast<int>(sh.ncand), CAP);
+
+    bitonic_desc(sh.cand, n);
+    return n;
+  };
+  // Narrow the whole row down to the decision point of a criterion.
+  auto narrow = [&](int crit, uint32_t rank, float mp, uint64_t thr, uint32_t tau) -> Narrow __attribute__((always_inline)) {
+    Narrow r = {OUT_NONE, 0, 0, 0, 0, 0, 0, 0};
+    Pick p = choose_bin(sh, sh.cnt1, sh.mass1, NB, 0u, 21, 0u, 0ull, crit, rank, mp, M, thr, tau);
+    if (p.bin < 0) return r;
+    uint32_t klo = static_cast<uint32_t>(p.bin) << 21;
+    int shift = 21;
+    uint32_t count = sh.cnt1[p.bin];
+    uint64_t rmass = sh.mass1[p.bin];
+    for (;;) {
+      const uint32_t khi = klo + ((1u << shift) - 1u);
+      r.klo = klo;
+      r.khi = khi;
+      r.n_ab = p.n_ex;
+      r.m_ab = p.m_ex;
+      r.count = count;
+      r.rmass = rmass;
+      if (count <= static_cast<uint32_t>(CAP)) {
+        r.n = collect(klo, khi);
+        r.out = OUT_CAND;
+        return r;
+      }
+      if (shift == 0) {
+        r.out = OUT_VALUE;
+        return r;
+      }
+      const int nshift = shift == 21 ? 10 : 0;
+      const int nb = shift == 21 ? NB : NB3;
+      hist_pass(sh.cnt, sh.mass, klo, nshift, nb);
+      const Pick q = choose_bin(sh, sh.cnt, sh.mass, nb, klo, nshift, p.n_ex, p.m_ex, crit, rank, mp, M, thr, tau);
+      if (q.bin < 0) {
+        r.out = OUT_ALLKEPT;
+        return r;
+      }
+      klo = klo + (static_cast<uint32_t>(q.bin) << nshift);
+      shift = nshift;
+      count = sh.cnt[q.bin];
+      rmass = sh.mass[q.bin];
+      p = q;
+      __syncthreads();
+    }
+  };
+  // Count and mass of the candidates [0, n) with key >= tau.
+  auto cand_sum = [&](int n, uint32_t tau, uint32_t& cnt_out, uint64_t& mass_out) __attribute__((always_inline)) {
+    uint32_t c = 0;
+    uint64_t m = 0;
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t v = sh.cand[i];
+      const uint32_t k = static_cast<uint32_t>(v >> 32);
+      if (k >= tau) {
+        ++c;
+        m += fx45(expf(f32_of_key(k) - M));
+      }
+    }
+    cnt_out = block_reduce<uint32_t>(c, OpAdd(), sh.redu);
+    mass_out = block_reduce<uint64_t>(m, OpAdd(), sh.redq);
+  };
+  // Index of the member of rank r (ascending index) among elements with key v.
+  auto find_rank = [&](uint32_t v, uint32_t r) -> int __attribute__((always_inline)) {
+    if (tid == 0) sh.result = -1;
+    __syncthreads();
+    uint32_t base = 0;
+    auto round = [&](uint32_t mbits, int c) -> bool {
+      uint32_t tot;
+      const uint32_t n = static_cast<uint32_t>(__popc(mbits));
+      const uint32_t ex = block_excl_scan<uint32_t>(n, sh.redu, &tot);
+      if (base + ex <= r && r < base + ex + n) {
+        uint32_t need = r - base - ex;
+        for (int e = 0; e < 4; ++e) {
+          if ((mbits >> e) & 1u) {
+            if (need == 0) {
+              sh.result = 4 * c + e;
+              break;
+            }
+            --need;
+          }
+        }
+      }
+      base += tot;
+      return base > r;
+    };
+    for (int c0 = 0; c0 < nch; c0 += NT) {
+      const int c = c0 + tid;
+      const float4 q = S.chunk(c);
+      const uint32_t hb = X.nibble(c);
+      const float xs[4] = {q.x, q.y, q.z, q.w};
+      uint32_t mb = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mb |= static_cast<uint32_t>(4 * c + e < V && f32_key(X.y(xs[e], (hb >> e) & 1u)) == v) << e;
+      if (round(mb, c)) break;
+    }
+
+    __syncthreads();
+    const int res = sh.result;
+    __syncthreads();
+    return res;
+  };
+
+  // ------------------------------------------------ decisions
+  // The kept set is a prefix of the order (descending key, ascending index):
+  // composite (key << 32 | ~index) >= CK.  tau = key bound of the value cuts.
+  uint32_t tau = KEY_MIN_FINITE;  // -inf entries are never kept
+  uint64_t CK = static_cast<uint64_t>(tau) << 32;
+  uint64_t keep_mass = 0;
+  uint32_t keep_n = 0;
+  int64_t tok = -1;
+
+  if (status == 0) {
+    hist_pass(sh.cnt1, sh.mass1, 0u, 21, NB);
+    uint32_t c = 0;
+    uint64_t m = 0;
+    for (int i = tid; i < NB; i += NT) {
+      m += sh.mass1[i];
+      if (static_cast<uint32_t>(i) >= (KEY_MIN_FINITE >> 21)) c += sh.cnt1[i];
+    }
+    keep_n = block_reduce<uint32_t>(c, OpAdd(), sh.redu);
+    keep_mass = block_reduce<uint64_t>(m, OpAdd(), sh.redq);
+  }
+
+  // Stages, in the reference's order: 0 top-k (sampling.py:36-38), 1 min-p
+  // (:40-43), 2 top-p (:45-51), 3 selection (:56-61).  One narrowing per
+  // stage; a stage whose decision falls inside a run of more than CAP equal
+  // values asks for the index of one member by rank.
+  for (int stage = 0; stage < 4; ++stage) {
+    if (stage == 2) {
+      CK = static_cast<uint64_t>(tau) << 32;
+      if (tau > kmax || keep_n == 0) status |= FL_ROW_ALL_MASKED;
+    }
+    if (status != 0) break;
+    bool active = false;
+    int crit = CRIT_COUNT;
+    uint32_t rank = 0, tr = 0;
+    float mp = 0.0f;
+    uint64_t thr = 0, target = 0;
+    if (stage == 0) {
+      active = K > 0 && K < V;
+      rank = static_cast<uint32_t>(K - 1);
+    } else if (stage == 1) {
+      active = MP > 0.0f;
+      crit = CRIT_PRED;
+      mp = MP;
+      tr = tau;
+    } else if (stage == 2) {
+      active = TP > 0.0f && TP < 1.0f;
+      crit = CRIT_MASS;
+      thr = static_cast<uint64_t>(ceil(static_cast<double>(TP) * static_cast<double>(keep_mass)));
+      tr = tau;
+    } else {
+      active = select;
+      if (T > 0.0f) {
+        crit = CRIT_MASS;
+        target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(keep_mass)));
+        thr = target + 1u;
+        tr = static_cast<uint32_t>(CK >> 32);
+      }
+    }
+    if (!active) continue;
+    const Narrow n = narrow(crit, rank, mp, thr, tr);
+
+    bool need_rank = false;
+    uint32_t rv = 0, rr = 0;
+    if (stage == 0) {
+      // k-th largest value; every element equal to it survives
+      uint32_t tk = 0;
+      if (n.out == OUT_CAND) tk = static_cast<uint32_t>(sh.cand[K - 1 - static_cast<int>(n.n_ab)] >> 32);
+      else if (n.out == OUT_VALUE) tk = n.klo;
+      if (tk > tau) {
+        tau = tk;
+        if (n.out == OUT_CAND) {
+          uint32_t c;
+          uint64_t m;
+          cand_sum(n.n, tau, c, m);
+          keep_n = n.n_ab + c;
+          keep_mass = n.m_ab + m;
+        } else {
+          keep_n = n.n_ab + n.count;
+          keep_mass = n.m_ab + n.rmass;
+        }
+      }
+    } else if (stage == 1) {
+      // smallest kept value: the passing candidates form a prefix
+      uint32_t tm = 0;
+      bool whole_range = false;
+      if (n.out == OUT_CAND) {
+        uint32_t c = 0;
+        for (int i = tid; i < n.n; i += NT) {
+          const uint32_t k = static_cast<uint32_t>(sh.cand[i] >> 32);
+          c += (k >= tau && expf(f32_of_key(k) - M) >= MP) ? 1u : 0u;
+        }
+        c = block_reduce<uint32_t>(c, OpAdd(), sh.redu);
+        tm = c > 0 ? static_cast<uint32_t>(sh.cand[c - 1] >> 32) : n.khi + 1u;
+      } else if (n.out == OUT_VALUE) {
+        tm = (expf(f32_of_key(n.klo) - M) >= MP) ? n.klo : n.klo + 1u;
+        whole_range = tm == n.klo;
+      } else if (n.out == OUT_ALLKEPT) {
+        tm = n.klo;
+        whole_range = true;
+      }
+      if (tm > tau) {
+        tau = tm;
+        if (n.out == OUT_CAND) {
+          uint32_t c;
+          uint64_t m;
+          cand_sum(n.n, tau, c, m);
+          keep_n = n.n_ab + c;
+          keep_mass = n.m_ab + m;
+        } else {
+          keep_n = n.n_ab + (whole_range ? n.count : 0u);
+          keep_mass = n.m_ab + (whole_range ? n.rmass : 0ull);
+        }
+      }
+    } else if (stage == 2) {
+      // first kept position whose exclusive mass reaches thr
+      if (n.out == OUT_CAND) {
+        const int per = (n.n + NT - 1) / NT;
+        const int i0 = min(n.n, tid * per), i1 = min(n.n, i0 + per);
+        uint64_t lm = 0;
+        for (int i = i0; i < i1; ++i) {
+          const uint32_t k = static_cast<uint32_t>(sh.cand[i] >> 32);
+          if (k >= tau) lm += fx45(expf(f32_of_key(k) - M));
+        }
+        uint64_t tot;
+        const uint64_t ex = block_excl_scan<uint64_t>(lm, sh.redq, &tot);
+        int first = INT_MAX;
+        uint64_t mass_before = 0;
+        uint64_t c = n.m_ab + ex;
+        for (int i = i0; i < i1; ++i) {
+          const uint32_t k = static_cast<uint32_t>(sh.cand[i] >> 32);
+          if (k < tau) break;  // candidates below tau follow every kept one
+          if (c >= thr) {
+            first = i;
+            mass_before = c;
+            break;
+          }
+          c += fx45(expf(f32_of_key(k) - M));
+        }
+        const int f = block_reduce<int32_t>(first, OpMin(), sh.redi);
+        if (f != INT_MAX) {
+          if (first == f) sh.bcast_q = mass_before;
+          __syncthreads();
+          CK = f == 0 ? static_cast<uint64_t>(n.khi + 1u) << 32 : sh.cand[f - 1];
+          keep_n = n.n_ab + static_cast<uint32_t>(f);
+          keep_mass = sh.bcast_q;
+          __syncthreads();
+        } else {
+          // no kept candidate is removed: the bin's mass reaches thr, so the
+          // first removed element is the next one after the bin
+          uint32_t nk = 0;
+          for (int i = tid; i < n.n; i += NT) nk += static_cast<uint32_t>(sh.cand[i] >> 32) >= tau ? 1u : 0u;
+          nk = block_reduce<uint32_t>(nk, OpAdd(), sh.redu);
+          if (nk > 0) {
+            CK = sh.cand[nk - 1];
+            keep_n = n.n_ab + nk;
+            keep_mass = n.m_ab + tot;
+          }
+        }
+      } else if (n.out == OUT_VALUE) {
+        // members of one value, in index order, each of mass fv
+        const uint32_t v = n.klo;
+        const uint64_t fv = fx45(expf(f32_of_key(v) - M));
+        uint64_t jstar = n.count;  // first removed member
+        if (n.m_ab >= thr) jstar = 0;
+        else if (fv > 0) jstar = (thr - n.m_ab + fv - 1) / fv;
+        if (jstar > n.count) jstar = n.count;
+        if (jstar == 0) CK = static_cast<uint64_t>(v + 1u) << 32;
+        else if (jstar == n.count) CK = static_cast<uint64_t>(v) << 32;  // the whole value stays
+        need_rank = jstar > 0 && jstar < n.count;
+        rv = v;
+        rr = static_cast<uint32_t>(jstar) - 1u;
+        keep_n = n.n_ab + static_cast<uint32_t>(jstar);
+        keep_mass = n.m_ab + jstar * fv;
+      }
+    } else {
+      if (T <= 0.0f) {
+        // greedy (sampling.py:59-60): first index of the maximal value
+        if (n.out == OUT_CAND) tok = static_cast<uint32_t>(~static_cast<uint32_t>(sh.cand[0]));
+        need_rank = n.out == OUT_VALUE;
+        rv = n.klo;
+        rr = 0;
+      } else if (n.out == OUT_CAND) {
+        // inverse CDF over the kept candidates
+        const int per = (n.n + NT - 1) / NT;
+        const int i0 = min(n.n, tid * per), i1 = min(n.n, i0 + per);
+        uint64_t lm = 0;
+        int last_kept = -1;
+        for (int i = i0; i < i1; ++i) {
+          if (sh.cand[i] >= CK) {
+            lm += fx45(expf(f32_of_key(static_cast<uint32_t>(sh.cand[i] >> 32)) - M));
+            last_kept = i;
+          }
+        }
+        uint64_t tot;
+        const uint64_t ex = block_excl_scan<uint64_t>(lm, sh.redq, &tot);
+        int first = INT_MAX;
+        uint64_t c = n.m_ab + ex;
+        for (int i = i0; i < i1; ++i) {
+          if (sh.cand[i] < CK) break;
+          c += fx45(expf(f32_of_key(static_cast<uint32_t>(sh.cand[i] >> 32)) - M));
+          if (c > target) {
+            first = i;
+            break;
+          }
+        }
+        int f = block_reduce<int32_t>(first, OpMin(), sh.redi);
+        // the target lies past the kept members of this bin only through the
+        // ceiling of the top-p threshold: take the last kept candidate
+        if (f == INT_MAX) f = block_reduce<int32_t>(last_kept, OpMax(), sh.redi);
+        if (f >= 0) tok = static_cast<uint32_t>(~static_cast<uint32_t>(sh.cand[f]));
+      } else if (n.out == OUT_VALUE) {
+        const uint32_t v = n.klo;
+        const uint64_t fv = fx45(expf(f32_of_key(v) - M));
+        uint32_t kept_cnt = n.count;  // members of this value inside the kept set
+        if (static_cast<uint32_t>(CK >> 32) == v && static_cast<uint32_t>(CK) != 0u) kept_cnt = keep_n - n.n_ab;
+        uint64_t j = 0;
+        if (fv > 0 && target >= n.m_ab) j = (target - n.m_ab) / fv;
+        if (j + 1 > kept_cnt) j = kept_cnt > 0 ? kept_cnt - 1 : 0;
+        need_rank = true;
+        rv = v;
+        rr = static_cast<uint32_t>(j);
+      }
+    }
+    if (need_rank) {
+      const int idx = find_rank(rv, rr);
+      if (stage == 2) CK = (static_cast<uint64_t>(rv) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(idx));
+      else tok = idx;
+    }
+    if (stage == 2 && keep_n == 0) status |= FL_ROW_ALL_MASKED;
+    if (stage == 3 && tok < 0) status |= FL_ROW_LIMIT;
+  }
+
+  const double SK = from_fx45(keep_mass);
+  const float rK = 1.0f / static_cast<float>(SK);
+  float y_sel = 0.0f;
+  if (tid == 0 && status == 0 && tok >= 0) {
+    const int i = static_cast<int>(tok);
+    y_sel = X.y(row[i], (X.nibble(i >> 2) >> (i & 3)) & 1u);
+  }
+
+  // ------------------------------------------------ outputs
+  if (tid == 0) {
+    if (status != 0) tok = -1;
+    if (a.out_token) a.out_token[b] = tok;
+    if (a.out_status) a.out_status[b] = status;
+    if (a.out_finished) {
+      const bool fin = (a.finished_in != nullptr && a.finished_in[b] != 0) ||
+                       (tok >= 0 && is_stop(a.stop_ids, a.stop_ld, a.n_stop, b, tok));
+      a.out_finished[b] = fin ? 1 : 0;
+    }
+    if (a.out_logprob) {
+      float lp = __builtin_nanf("");
+      if (tok >= 0) lp = (y_sel - M) - logf(static_cast<float>(SK));
+      a.out_logprob[b] = lp;
+    }
+    if (a.out_desc) {
+      fl_row_desc dsc;
+      dsc.status = status;
+      dsc.shift = M;
+      dsc.mass = SK;
+      dsc.inv_mass = rK;
+      if (status == 0) {
+        const uint32_t low = static_cast<uint32_t>(CK);
+        dsc.y_cut = f32_of_key(static_cast<uint32_t>(CK >> 32));
+        dsc.idx_cut = low == 0u ? INT_MAX : static_cast<int32_t>(~low);
+        dsc.n_kept = static_cast<int32_t>(keep_n);
+      } else {
+        dsc.y_cut = __builtin_inff();
+        dsc.idx_cut = -1;
+        dsc.n_kept = 0;
+      }
+      a.out_desc[b] = dsc;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launch
+hipError_t launch_sample_rows32(const fl_sample_args& a, hipStream_t s) {
+  const size_t dyn = a.hist_ids != nullptr ? static_cast<size_t>((a.vocab + 31) / 32) * 4u : 0u;
+  hipLaunchKernelGGL(k_sample_rows32, dim3(static_cast<unsigned>(a.batch)), dim3(NT), dyn, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace fl
