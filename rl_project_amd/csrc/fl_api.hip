@@ -104,8 +104,11 @@ int fl_spec_verify(const fl_spec_args* a, void* stream) {
     return fail(FL_EINVAL, "fl_spec_verify: bad shape batch=%lld k=%lld vocab=%lld ld=%lld",
                 static_cast<long long>(a->batch), static_cast<long long>(a->k), static_cast<long long>(a->vocab),
                 static_cast<long long>(a->ld));
+  if (a->vocab > FL_MAX_VOCAB_F32 || a->batch > 0x7fffffff)
+    return fail(FL_ENOTSUP, "fl_spec_verify: vocab %lld or batch %lld beyond this build's limits",
+                static_cast<long long>(a->vocab), static_cast<long long>(a->batch));
   if (a->batch == 0) return ok();
-  if (!a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
+  if (!a->temperature || !a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
       !a->u_resample || !a->bonus_token || !a->out_n_accepted || !a->out_tokens)
     return fail(FL_EINVAL, "fl_spec_verify: a required pointer is NULL");
   const hipError_t e = fl::launch_spec_verify(*a, static_cast<hipStream_t>(stream));

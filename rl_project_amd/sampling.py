@@ -123,9 +123,10 @@ def _stop_tensor(stop_ids, B: int, device: torch.device) -> Tuple[Optional[torch
 class _Call:
     """Argument block of one fl_sample call with the tensors it points to."""
 
-    def __init__(self, logits: torch.Tensor, *, temperature: PerRow, top_k: PerRow, top_p: PerRow, min_p: PerRow,
-                 repetition_penalty: PerRow, history, stop_ids, uniforms: Optional[torch.Tensor],
-                 finished: Optional[torch.Tensor], softcap: float, flags: int, want_logprob: bool, want_desc: bool):
+    def __init__(self, logits: torch.Tensor, *, temperature: PerRow = 1.0, top_k: PerRow = None,
+                 top_p: PerRow = None, min_p: PerRow = None, repetition_penalty: PerRow = 1.0, history=None,
+                 stop_ids=None, uniforms: Optional[torch.Tensor] = None, finished: Optional[torch.Tensor] = None,
+                 softcap: float = 0.0, flags: int = 0, want_logprob: bool = False, want_desc: bool = False):
         self.logits = logits = _check_logits(logits)
         B, V = logits.shape
         dev = logits.device
