@@ -81,8 +81,9 @@ typedef struct fl_row_desc {
 
 /*
  * Arguments of one batched sampling call.  Row b's logits start at
- * logits + b * ld elements.  Per-row parameter arrays have `batch` entries;
- * a parameter at its "off" value disables that stage for that row:
+ * logits + b * ld elements.  The five per-row parameter arrays (temperature,
+ * top_k, top_p, min_p, rep_penalty) are required and have `batch` entries; a
+ * parameter at its "off" value disables that stage for that row:
  *   temperature <= 0  -> no scaling, greedy selection (sampling.py:33, :59)
  *   top_k <= 0        -> off (sampling.py:36)
  *   top_p outside (0,1) -> off (sampling.py:45)
@@ -92,7 +93,10 @@ typedef struct fl_row_desc {
  * (ids may repeat; presence, not frequency, is penalised).  Stop ids: row b's
  * stop set is stop_ids[b*stop_ld : b*stop_ld + n_stop]; stop_ld == 0 shares
  * one set; entries < 0 are ignored.  uniforms[b] in [0, 1) drives row b's
- * selection.  finished_in may be NULL.  out_logprob and out_desc may be NULL.
+ * selection (required unless FL_FLAG_NO_SELECT; values outside are clamped).
+ * hist_ids may be NULL (no penalty anywhere); if not, hist_len is required and
+ * hist_ld == 0 shares one id list between all rows.  finished_in may be NULL.
+ * out_logprob, out_status, out_finished and out_desc may be NULL.
  */
 typedef struct fl_sample_args {
   uint32_t struct_size;        /* sizeof(fl_sample_args) */
