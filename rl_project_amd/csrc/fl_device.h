@@ -18,12 +18,18 @@
 // Phase timestamps for kernel tuning builds (-DFL_PHASE_TIMES): thread 0 of
 // work-groups 0..3 records the constant-rate wall clock at each FL_MARK.
 #ifdef FL_PHASE_TIMES
-static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64];
+// [0, 192): marks of blocks 0..3; [192, 192 + 2*1024): start / end of every block
+static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64 + 2 * 1024];
 #define FL_MARK(n)                                                              \
   do {                                                                          \
-    if (blockIdx.x < 4 && threadIdx.x == 0) {                                   \
-      fl_phase_ts[blockIdx.x * 16 + (n)] = wall_clock64();                      \
-      fl_phase_ts[64 + blockIdx.x * 16 + (n)] = clock64();                      \
+    if (threadIdx.x == 0) {                                                     \
+      const uint64_t t_ = wall_clock64();                                       \
+      if (blockIdx.x < 4) {                                                     \
+        fl_phase_ts[blockIdx.x * 16 + (n)] = t_;                                \
+        fl_phase_ts[64 + blockIdx.x * 16 + (n)] = clock64();                    \
+      }                                                                         \
+      if (((n) == 0 || (n) == 9) && blockIdx.x < 1024)                          \
+        fl_phase_ts[192 + 2 * blockIdx.x + ((n) == 9)] = t_;                    \
     }                                                                           \
   } while (0)
 #else
@@ -121,7 +127,18 @@ __device__ __forceinline__ float temperature_val(float x, float t) {
 // associative (deterministic scans), and stay below 2^53 so that converting a
 // sum back to double is exact.
 constexpr double FX_ONE = 70368744177664.0;  // 2^46
-__device__ __forceinline__ uint64_t to_fx(float p) { return __double2ull_rn(static_cast<double>(p) * FX_ONE); }
+// round(p * 2^46) for p in [0, 1] from the float's fields (ties round up);
+// integer arithmetic only
+__device__ __forceinline__ uint64_t to_fx(float p) {
+  const uint32_t u = __float_as_uint(p);
+  const int ex = static_cast<int>(u >> 23);
+  if (ex == 0) return 0;  // zero or denormal (< 2^-126): below the resolution
+  const uint64_t m = (u & 0x7FFFFFu) | 0x800000u;  // p = m * 2^(ex - 150)
+  const int s = ex - 150 + 46;
+  if (s >= 0) return m << s;
+  if (s < -24) return 0;
+  return (m + (1ull << (-s - 1))) >> (-s);
+}
 __device__ __forceinline__ double from_fx(uint64_t v) { return static_cast<double>(v) * (1.0 / FX_ONE); }
 
 // Work-group barrier that orders LDS only: waits for this wave's LDS
@@ -196,6 +213,68 @@ __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
   __syncthreads();
   *total = tot;
   return base + exc;
+}
+
+// Exclusive prefix sums of two quantities in thread order with one pair of
+// barriers; ta / tb receive the totals.
+__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_t* ra, uint64_t* rb, uint32_t& ea,
+                                                 uint64_t& eb, uint32_t& ta, uint64_t& tb) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int w = threadIdx.x / WAVE;
+  const uint32_t ia = wave_incl_scan(a);
+  const uint64_t ib = wave_incl_scan(b);
+  uint32_t xa = shfl_up(ia, 1);
+  uint64_t xb = shfl_up(ib, 1);
+  if (lane == 0) {
+    xa = 0;
+    xb = 0;
+  }
+  if (lane == WAVE - 1) {
+    ra[w] = ia;
+    rb[w] = ib;
+  }
+  __syncthreads();
+  uint32_t ba = 0, sa = 0;
+  uint64_t bb = 0, sb = 0;
+#pragma unroll
+  for (int i = 0; i < NWAVE; ++i) {
+    const uint32_t x = ra[i];
+    const uint64_t y = rb[i];
+    if (i < w) {
+      ba += x;
+      bb += y;
+    }
+    sa += x;
+    sb += y;
+  }
+  __syncthreads();
+  ea = ba + xa;
+  eb = bb + xb;
+  ta = sa;
+  tb = sb;
+}
+
+// First index i in [a, b) with pred(i) true, for a predicate that is false
+// then true along the range (b if it never holds).  The 64 lanes of a wave
+// probe 64 evenly spaced indices per step, so a range of n needs about
+// log64(n) + 1 steps; every wave computes the same result, without barriers.
+template <class P>
+__device__ __forceinline__ int wave_first(int a, int b, P&& pred) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  for (;;) {
+    const int s = max(1, (b - a + WAVE - 1) / WAVE);
+    const int p = a + lane * s;
+    const uint64_t m = __ballot(p < b && pred(p));
+    if (s == 1) return m ? a + __ffsll(static_cast<unsigned long long>(m)) - 1 : b;
+    if (m == 0) {
+      a += min(WAVE - 1, (b - a - 1) / s) * s + 1;  // past the last probe inside [a, b)
+    } else {
+      const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+      if (f == 0) return a;
+      b = a + f * s;
+      a = a + (f - 1) * s + 1;
+    }
+  }
 }
 
 // Indices held by this thread for a slice partition of n items.

@@ -31,10 +31,17 @@ constexpr int NCH = 16;                          // 16-byte chunks per thread
 constexpr int HIST_WORDS = 32768;                // 65536 packed u16 counters
 constexpr int HBITS_WORDS = FL_MAX_VOCAB_16 / 32;
 constexpr int OWNER_WORDS = FL_MAX_HISTORY / 32;
-constexpr int LIST_CAP = 3 * HIST_WORDS / 8;     // candidates per identification target
-constexpr int HIT_CAP = HIST_WORDS / 4;          // queued chunks with a candidate (after the two lists)
-constexpr int ENTRY_CACHE_MAX = HIST_WORDS / 3;  // entries whose y and e fit beside the list
-constexpr int RANK_SELECT_MAX = 2048;            // candidates ranked by all-pairs counting
+constexpr int LIST_CAP = HIST_WORDS / 4;          // candidates per identification target
+constexpr int HIT_CAP = (HIST_WORDS / 2) / 5;     // queued chunks (index + 4 data words), after the lists
+constexpr int RANK_BINS = FL_MAX_VOCAB_16 / 128;  // index buckets of the rank selection
+constexpr int SLICE_BASE = HIST_WORDS - 5 * NT;   // slice tables: count u32[NT], mass u64[NT], scan u64[NT]
+constexpr int ENT_MAX = SLICE_BASE;               // entries (distinct values) a row may have
+constexpr int YE_CACHE_MAX = ENT_MAX / 3;         // entries whose y and e are kept beside them
+constexpr int CUM_MAX = ENT_MAX / 5 - 1;          // ... and also a 64-bit cumulative per entry
+constexpr int CUM_PER = 8;                        // most entries per thread with the cumulative kept
+// order block (4096 orders) handled by each wave: the blocks real logits
+// populate go to waves on different SIMDs (wave w runs on SIMD w % 4)
+__constant__ const int kBlockOfWave[16] = {3, 4, 11, 12, 5, 13, 0, 1, 2, 6, 7, 8, 9, 10, 14, 15};
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 
 static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
@@ -43,21 +50,19 @@ struct Shared16 {
   uint32_t hist[HIST_WORDS];
   uint32_t hbits[HBITS_WORDS];
   uint32_t owner[OWNER_WORDS];
-  double redd[NWAVE];
   uint64_t redq[NWAVE];
   uint32_t redu[NWAVE];
-  uint32_t redi_u[NWAVE];
-  int32_t redi[NWAVE];
   int32_t status;
-  int32_t n_entries;
-  int32_t ik, lk;
-  int32_t i0;
-  uint32_t c0;
-  int32_t sel_entry;
-  uint64_t sel_cexcl;
   int32_t result[2];
+  struct {
+    double S, SK;
+    int32_t L, i0, cut_lo, cut_hi, sel_lo, sel_hi;
+    uint32_t c0, cut_kept, cut_total, n_kept, sel_rank;
+    float y_sel, y_cut;
+  } dec;  // decisions of the search wave
   uint32_t nlist[2];
   uint32_t nhit;
+  uint32_t rank_bin, rank_in_bin;
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -75,6 +80,29 @@ __device__ __forceinline__ uint4 load_chunk16(const uint16_t* row, int c, int V,
     w[k] = lo | (hi << 16);
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Value transforms of the rarer paths (soft-cap, values rebuilt from orders)
+// are kept out of line: inlined at every call site they would multiply the
+// kernel's code.  The penalty is small and on the common path: inline.
+template <class D>
+__device__ __noinline__ uint32_t capped_bits(uint32_t raw, float cap) {
+  return D::from_f32(softcap_val<D>(D::to_f32(raw), cap));
+}
+template <class D>
+__device__ __forceinline__ uint32_t penalised_bits(uint32_t z, float rp) {
+  return D::from_f32(penalty_val<D>(D::to_f32(z), rp));
+}
+// filtered value of a pattern given as an order index (soft-cap if `sc`)
+template <class D>
+__device__ __noinline__ float value_of_order(uint32_t order, float cap, float t, bool sc) {
+  float z = D::to_f32(bits_of_order16(order));
+  if (sc) z = softcap_val<D>(z, cap);
+  return temperature_val<D>(z, t);
+}
+template <class D>
+__device__ __noinline__ float e_of_order(uint32_t order, float cap, float t, bool sc, float M) {
+  return expf(value_of_order<D>(order, cap, t, sc) - M);
 }
 
 }  // namespace
@@ -132,8 +160,15 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     sh.nlist[0] = sh.nlist[1] = 0;
     sh.nhit = 0;
     sh.result[0] = sh.result[1] = -1;
-    sh.ik = 0;
-    sh.lk = 0;
+    sh.dec.L = 0;
+    sh.dec.i0 = -1;
+    sh.dec.c0 = 0;
+    sh.dec.S = sh.dec.SK = 0.0;
+    sh.dec.cut_lo = sh.dec.cut_hi = sh.dec.sel_lo = 0;
+    sh.dec.sel_hi = -1;
+    sh.dec.cut_kept = sh.dec.cut_total = sh.dec.n_kept = sh.dec.sel_rank = 0;
+    sh.dec.y_sel = 0.0f;
+    sh.dec.y_cut = __builtin_inff();
   }
   lds_barrier();
   FL_MARK(1);
@@ -158,7 +193,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 
   // Value pattern of an element as the filters see it before penalty.
   auto elem_bits = [&](uint32_t raw) -> uint32_t {
-    return SC_ELEM ? D::from_f32(softcap_val<D>(D::to_f32(raw), CAP)) : raw;
+    return SC_ELEM ? capped_bits<D>(raw, CAP) : raw;
   };
 
   // ------------------------------------------------ history: unique ids
@@ -186,7 +221,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
 
   // ------------------------------------------------ count patterns
-  auto count = [&](uint32_t bits) { atomicAdd(&sh.hist[bits >> 1], (bits & 1u) ? 0x10000u : 1u); };
+  auto count = [&](uint32_t bits) { atomicAdd(&sh.hist[bits >> 1], 1u + (bits & 1u) * 0xFFFFu); };
   if (fast) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -212,7 +247,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // each unique id moves one count from its pattern to its penalised pattern
   auto penalise = [&](uint32_t raw) {
     const uint32_t z = elem_bits(raw);
-    const uint32_t zp = D::from_f32(penalty_val<D>(D::to_f32(z), RP));
+    const uint32_t zp = penalised_bits<D>(z, RP);
     if (zp != z) {
       atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
       atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
@@ -229,343 +264,369 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   FL_MARK(2);
 
   // ------------------------------------------------ compact to entries
-  // Wave w owns order indices [4096w, 4096w+4096): waves 0-7 the positive
-  // patterns (descending bits), 8-15 the negative ones (ascending bits).  Lane
-  // l reads word 64i+l of its wave's range in step i, so the 64 lanes of a
-  // read hit consecutive LDS words (no bank conflicts); a word's two
-  // counters are two consecutive order indices.  Positions come from ballots:
-  // entries are written in ascending order index.
+  // Order o = 0 is the largest value.  Wave w owns the 4096 orders of block
+  // kBlockOfWave[w]; in step i lane l reads the word of orders
+  // block*4096 + 128i + 2l and +1, so a wave's 64 reads hit 64 consecutive
+  // LDS words (no bank conflicts) and its entries for step i are consecutive
+  // (positions from ballots).  The permutation puts the blocks that real
+  // logits populate (|x| in about [2^-32, 2^32]: blocks 3-5 and 11-13) on
+  // different SIMDs.
+  int N;
   {
     const int wave = tid / WAVE;
     const int lane = tid & (WAVE - 1);
-    const bool pos = wave < NWAVE / 2;  // wave-uniform
+    const int blk = kBlockOfWave[wave];
+    const bool posb = blk < NWAVE / 2;  // positive values (wave-uniform)
+    const uint32_t ob = 4096u * blk;
     uint32_t x[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      const int W = pos ? (0x3FFF - 2048 * wave - (64 * i + lane)) : (2048 * wave + 64 * i + lane);
-      x[i] = sh.hist[W];
+      // word of orders ob + 128i + 2l (first half after the swap) and + 1
+      const int W = posb ? (0x3FFF - 2048 * blk - 64 * i - lane) : (2048 * blk + 64 * i + lane);
+      const uint32_t w = sh.hist[W];
+      x[i] = posb ? __builtin_amdgcn_alignbit(w, w, 16) : w;
+    }
+    // NaN patterns occupy the two ends of the order (the first steps of block
+    // 0, the last steps of block 15): drop them, flag the row
+    constexpr int NAN_STEPS = (0x8000 - static_cast<int>(D::INF_BITS) + 127) / 128;
+    if (blk == 0 || blk == NWAVE - 1) {
+      bool nan = false;
+#pragma unroll
+      for (int k = 0; k < NAN_STEPS; ++k) {
+        const int i = blk == 0 ? k : 31 - k;
+        uint32_t xi = x[0];
+#pragma unroll
+        for (int j = 1; j < 32; ++j) xi = (j == i) ? x[j] : xi;  // static-index select
+        const uint32_t o = ob + 128u * i + 2u * lane;
+        uint32_t keep = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t oh = o + h;
+          const bool is_nan = posb ? (oh < 0x7FFFu - D::INF_BITS) : (oh > 0x8000u + D::INF_BITS);
+          keep |= is_nan ? 0u : (h ? 0xFFFF0000u : 0x0000FFFFu);
+        }
+        nan |= (xi & ~keep) != 0u;
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          if (j == i) x[j] &= keep;
+      }
+      if (nan) atomicOr(&sh.status, FL_ROW_NAN);
     }
     uint32_t any = 0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) any |= x[i];
-    const bool populated = __ballot(any != 0) != 0;  // wave-uniform
-    // halves in ascending order index: positive words hi then lo, negative lo then hi
-    auto first = [&](uint32_t w) { return pos ? (w >> 16) : (w & 0xFFFFu); };
-    auto second = [&](uint32_t w) { return pos ? (w & 0xFFFFu) : (w >> 16); };
-    auto word_of = [&](int i) { return pos ? (0x3FFF - 2048 * wave - (64 * i + lane)) : (2048 * wave + 64 * i + lane); };
-    // bits of the first / second half of word W
-    auto bits1 = [&](int W) { return pos ? 2u * W + 1 : 2u * W; };
-    auto bits2 = [&](int W) { return pos ? 2u * W : 2u * W + 1; };
-    const bool nan_range = wave == 0 || wave == NWAVE - 1;  // all NaN patterns live here
-    auto valid = [&](uint32_t cnt, uint32_t bits) {
-      return cnt != 0 && (!nan_range || (bits & 0x7FFFu) <= D::INF_BITS);
-    };
-    uint32_t wtot = 0, lsum = 0;
-    bool nan = false;
-    if (populated && !nan_range) {
-      // SWAR: bit 15 / bit 31 set iff the low / high counter is non-zero
-      uint32_t lcnt = 0;
+    uint32_t wtot = 0;  // entries of this wave (wave-uniform)
+    if (__ballot(any != 0u) != 0) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        lcnt += __popc((((x[i] & 0x7FFF7FFFu) + 0x7FFF7FFFu) | x[i]) & 0x80008000u);
-        lsum += (x[i] & 0xFFFFu) + (x[i] >> 16);
-      }
-      wtot = wave_reduce(lcnt, OpAdd());
-    } else if (populated) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const int W = word_of(i);
-        const uint32_t a1 = first(x[i]), a2 = second(x[i]);
-        const bool v1 = valid(a1, bits1(W)), v2 = valid(a2, bits2(W));
-        nan |= (a1 != 0 && !v1) || (a2 != 0 && !v2);
-        wtot += __popcll(__ballot(v1)) + __popcll(__ballot(v2));
-        lsum += a1 + a2;
-      }
+      for (int i = 0; i < 32; ++i)
+        wtot += __popcll(__ballot((x[i] & 0xFFFFu) != 0u)) + __popcll(__ballot((x[i] >> 16) != 0u));
     }
-    if (nan) atomicOr(&sh.status, FL_ROW_NAN);
-    if (lane == 0) sh.redu[wave] = wtot;
-    const uint32_t total_cnt = block_reduce<uint32_t>(lsum, OpAdd(), sh.redi_u);  // includes a barrier
-    uint32_t base = 0, n_total = 0;
+    if (lane == 0) sh.redu[blk] = wtot;
+    __syncthreads();
+    uint32_t base = 0, tot = 0;
 #pragma unroll
-    for (int i = 0; i < NWAVE; ++i) {
-      const uint32_t t = sh.redu[i];
-      if (i < wave) base += t;
-      n_total += t;
+    for (int k = 0; k < NWAVE; ++k) {
+      const uint32_t t = sh.redu[k];
+      if (k < blk) base += t;
+      tot += t;
     }
     if (wtot) {
+      // branch-free: an empty half writes to this lane's spare slot past the
+      // entry area instead of being skipped
+      const uint32_t spare = ENT_MAX + 2u * lane;
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        if (__ballot(x[i] != 0) == 0) continue;  // 64 empty words (wave-uniform)
-        const int W = word_of(i);
-        const uint32_t a1 = first(x[i]), a2 = second(x[i]);
-        const bool v1 = valid(a1, bits1(W)), v2 = valid(a2, bits2(W));
-        const uint64_t m1 = __ballot(v1), m2 = __ballot(v2);
-        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0)) +
-                               __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
+        const uint32_t a1 = x[i] & 0xFFFFu, a2 = x[i] >> 16;
+        const uint64_t m1 = __ballot(a1 != 0u), m2 = __ballot(a2 != 0u);
+        const uint32_t below =
+            __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32),
+                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0)) +
+            __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32),
+                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
+        const uint32_t o = ob + 128u * i + 2u * lane;
         const uint32_t p1 = base + below;
-        if (v1 && p1 < static_cast<uint32_t>(HIST_WORDS)) sh.hist[p1] = (order16(bits1(W)) << 16) | a1;
-        const uint32_t p2 = p1 + (v1 ? 1u : 0u);
-        if (v2 && p2 < static_cast<uint32_t>(HIST_WORDS)) sh.hist[p2] = (order16(bits2(W)) << 16) | a2;
-        base += __popcll(m1) + __popcll(m2);
+        const uint32_t p2 = p1 + (a1 ? 1u : 0u);
+        sh.hist[(a1 && p1 < static_cast<uint32_t>(ENT_MAX)) ? p1 : spare] = (o << 16) | a1;
+        sh.hist[(a2 && p2 < static_cast<uint32_t>(ENT_MAX)) ? p2 : spare + 1u] = ((o + 1u) << 16) | a2;
+        base += static_cast<uint32_t>(__popcll(m1) + __popcll(m2));
       }
     }
-    if (tid == 0) {
-      sh.n_entries = static_cast<int32_t>(min(n_total, static_cast<uint32_t>(HIST_WORDS)));
-      // a total other than V means a 16-bit counter wrapped (> 65535 equal values)
-      if (total_cnt != static_cast<uint32_t>(V) || n_total > static_cast<uint32_t>(HIST_WORDS))
-        sh.status |= FL_ROW_LIMIT;
-    }
+    N = static_cast<int>(min(tot, static_cast<uint32_t>(ENT_MAX)));
+    if (tid == 0 && tot > static_cast<uint32_t>(ENT_MAX)) atomicOr(&sh.status, FL_ROW_LIMIT);
   }
   __syncthreads();
   FL_MARK(3);
 
-  const int N = sh.n_entries;
+  // ------------------------------------------------ entry values
+  // Entry i: order ent[i] >> 16, count ent[i] & 0xFFFF, value Y(i) after
+  // soft-cap and temperature, E(i) = exp(Y(i) - M), cached beside the list
+  // when it fits.  Thread t owns the contiguous slice [t*per, t*per + per);
+  // the slice tables hold the count and the fixed-point mass before each
+  // slice, so any prefix sum is a table read plus fewer than `per` terms.
   uint32_t* ent = sh.hist;
-  const bool cached = N <= ENTRY_CACHE_MAX;
+  const bool cached = N <= YE_CACHE_MAX;
   float* Yc = reinterpret_cast<float*>(sh.hist + N);
   float* Ec = reinterpret_cast<float*>(sh.hist + 2 * N);
+  uint32_t* SliceCnt = sh.hist + SLICE_BASE;
+  uint64_t* SliceM = reinterpret_cast<uint64_t*>(sh.hist + SLICE_BASE + NT);
+  uint64_t* SliceX = reinterpret_cast<uint64_t*>(sh.hist + SLICE_BASE + 3 * NT);
+  const int per = max(1, (N + NT - 1) / NT);
+  // exclusive cumulative (p- or q-mass) per entry, when it fits: a search
+  // probe is then one read instead of a walk through its slice
+  const bool cum_ok = N <= CUM_MAX && per <= CUM_PER;
+  uint64_t* CumX = reinterpret_cast<uint64_t*>(sh.hist + ((3 * N + 1) & ~1));
+  const int lo = min(N, tid * per), hi = min(N, lo + per);
 
-  auto ent_cnt = [&](int i) -> uint32_t { return ent[i] & 0xFFFFu; };
-  auto ent_y = [&](int i) -> float {
-    float z = D::to_f32(bits_of_order16(ent[i] >> 16));
-    if (sc_entry) z = softcap_val<D>(z, CAP);
-    return temperature_val<D>(z, T);
-  };
-
-  float M = 0.0f;
-  if (sh.status == 0 && N > 0) {
-    M = ent_y(0);
-    if (tid == 0) {
-      if (isnan(M)) sh.status |= FL_ROW_NAN;
-      else if (isinf(M)) sh.status |= (M > 0.0f) ? FL_ROW_INF : FL_ROW_ALL_MASKED;
+  auto cnt_of = [&](int i) -> uint32_t { return ent[i] & 0xFFFFu; };
+  auto y_raw = [&](int i) -> float { return value_of_order<D>(ent[i] >> 16, CAP, T, sc_entry); };
+  const float M = N > 0 ? y_raw(0) : 0.0f;
+  if (tid == 0) {
+    if (N == 0 || isnan(M)) sh.status |= FL_ROW_NAN;
+    else if (isinf(M)) sh.status |= (M > 0.0f) ? FL_ROW_INF : FL_ROW_ALL_MASKED;
+  }
+  auto Y = [&](int i) -> float { return cached ? Yc[i] : y_raw(i); };
+  auto E = [&](int i) -> float { return cached ? Ec[i] : e_of_order<D>(ent[i] >> 16, CAP, T, sc_entry, M); };
+  {
+    uint32_t lc = 0;
+    uint64_t lm = 0;
+    for (int i = lo; i < hi; ++i) {
+      const uint32_t ord = ent[i] >> 16;
+      const float y = sc_entry ? value_of_order<D>(ord, CAP, T, true)
+                               : temperature_val<D>(D::to_f32(bits_of_order16(ord)), T);
+      const float e = expf(y - M);
+      if (cached) {
+        Yc[i] = y;
+        Ec[i] = e;
+      }
+      const uint32_t c = cnt_of(i);
+      lc += c;
+      lm += c * to_fx(e);
     }
+    uint32_t ec, tc;
+    uint64_t em, tm;
+    block_excl_scan2(lc, lm, sh.redu, sh.redq, ec, em, tc, tm);
+    SliceCnt[tid] = ec;
+    SliceM[tid] = em;
+    // a total other than V means a 16-bit counter wrapped (> 65535 equal values)
+    if (tid == 0 && tc != static_cast<uint32_t>(V)) atomicOr(&sh.status, FL_ROW_LIMIT);
   }
   __syncthreads();
   int32_t status = sh.status;
-
-  int lo, hi;
-  thread_slice(N, lo, hi);
-  if (status == 0 && cached) {
-    for (int i = lo; i < hi; ++i) {
-      const float y = ent_y(i);
-      Yc[i] = y;
-      Ec[i] = expf(y - M);
-    }
-  }
-  __syncthreads();
   FL_MARK(4);
-  auto Y = [&](int i) -> float { return cached ? Yc[i] : ent_y(i); };
-  auto E = [&](int i) -> float { return cached ? Ec[i] : expf(ent_y(i) - M); };
 
-  // Decision results (block-uniform once computed)
-  int i0 = N - 1;            // last entry that holds kept members
-  uint32_t c0 = 0;           // kept members of entry i0
-  double SK = 0.0;           // sum of e over kept members
-  uint32_t n_kept = 0;       // number of kept members
-  float rK = 0.0f;           // float32 reciprocal of SK (softmax scale)
-  int cut_lo = 0, cut_hi = 0;            // entries of i0's value group
-  uint32_t cut_kept = 0, cut_total = 0;  // kept / all members of that group
-  int sel_lo = 0, sel_hi = -1;           // entries of the selected value group
-  uint32_t sel_rank = 0;                 // rank by index within that group
+  auto count_before = [&](int L) -> uint32_t {
+    const int s = min(L / per, NT - 1);
+    uint32_t c = SliceCnt[s];
+    for (int i = s * per; i < L; ++i) c += cnt_of(i);
+    return c;
+  };
+  auto mass_before = [&](int L) -> uint64_t {
+    const int s = min(L / per, NT - 1);
+    uint64_t m = SliceM[s];
+    for (int i = s * per; i < L; ++i) m += cnt_of(i) * to_fx(E(i));
+    return m;
+  };
+  const bool w0 = tid < WAVE;  // the wave that runs the searches (results go through sh.dec)
 
+  // ---------------- top-k (sampling.py:36-38) and min-p (:40-43): value cuts
   if (status == 0) {
-    // ---------------- top-k (sampling.py:36-38): k-th largest value, ties kept
-    int L = N;
-    if (K > 0 && K < V) {
-      uint32_t local = 0;
-      for (int i = lo; i < hi; ++i) local += ent_cnt(i);
-      uint32_t tot;
-      uint32_t acc = block_excl_scan<uint32_t>(local, sh.redu, &tot);
-      if (acc < static_cast<uint32_t>(K) && acc + local >= static_cast<uint32_t>(K)) {
-        for (int i = lo; i < hi; ++i) {
-          acc += ent_cnt(i);
-          if (acc >= static_cast<uint32_t>(K)) { sh.ik = i; break; }
+    if (w0) {
+      int L = N;
+      if (K > 0 && K < V) {
+        // first entry whose inclusive count reaches K; every equal value stays
+        const int ik = wave_first(0, N, [&](int i) { return count_before(i + 1) >= static_cast<uint32_t>(K); });
+        const float tau = Y(ik);
+        L = wave_first(ik + 1, N, [&](int i) { return Y(i) < tau; });
+      }
+      double S = from_fx(mass_before(L));
+      if (MP > 0.0f) {
+        const float r = 1.0f / static_cast<float>(S);
+        const float thr = D::rn(D::rn(r) * MP);
+        const int Lm = wave_first(0, L, [&](int i) { return D::rn(E(i) * r) < thr; });
+        if (Lm < L) {
+          L = Lm;
+          S = from_fx(mass_before(L));
         }
       }
-      if (tid == 0) sh.lk = N;
-      __syncthreads();
-      const float tau = Y(sh.ik);
-      for (int i = max(lo, 1); i < hi; ++i)
-        if (Y(i) < tau && Y(i - 1) >= tau) sh.lk = i;
-      __syncthreads();
-      L = sh.lk;
-    }
-
-    // ---------------- min-p (sampling.py:40-43) over the top-k survivors
-    auto mass_upto = [&](int n) -> double {
-      double s = 0.0;
-      for (int i = lo; i < min(hi, n); ++i) s += static_cast<double>(ent_cnt(i)) * E(i);
-      return block_reduce<double>(s, OpAdd(), sh.redd);
-    };
-    double S = mass_upto(L);
-    if (MP > 0.0f) {
-      const float r = 1.0f / static_cast<float>(S);
-      const float thr = D::rn(D::rn(r) * MP);
-      int first_out = L;
-      for (int i = lo; i < min(hi, L); ++i)
-        if (D::rn(E(i) * r) < thr) { first_out = i; break; }
-      const int Lm = block_reduce<int32_t>(first_out, OpMin(), sh.redi);
-      if (Lm < L) {
-        L = Lm;
-        S = mass_upto(L);
+      if (tid == 0) {
+        sh.dec.L = L;
+        sh.dec.S = S;
       }
     }
-    if (L <= 0) status |= FL_ROW_ALL_MASKED;
+    __syncthreads();
+  }
+  FL_MARK(5);
+  int L = sh.dec.L;
+  if (status == 0 && L <= 0) status |= FL_ROW_ALL_MASKED;
+  FL_MARK(11);
 
-    // ---------------- top-p (sampling.py:45-51)
-    // Position j (descending order) is removed when
-    //   round(round_f32(C_j) - p_j) >= round(top_p)
-    // with C_j the inclusive cumulative of the rounded probabilities.  The
-    // predicate is monotone along the order, so the kept set is a prefix.
-    i0 = L - 1;
-    if (status == 0) c0 = ent_cnt(i0);
-    if (status == 0 && TP > 0.0f && TP < 1.0f) {
-      // cumulative sums in 2^-46 fixed point: exact, so every thread's slice
-      // boundaries agree with the block scan
+  // ---------------- top-p (sampling.py:45-51)
+  // Position j (descending order) is removed when
+  //   round(round_f32(C_j) - p_j) >= round(top_p)
+  // with C_j the inclusive cumulative of the rounded probabilities.  The
+  // predicate is monotone along the order, so the kept set is a prefix.
+  if (status == 0) {
+    const double S = sh.dec.S;
+    if (TP > 0.0f && TP < 1.0f) {
       const float r1 = 1.0f / static_cast<float>(S);
       const float t = D::rn(TP);
+      auto pf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * r1)); };
       auto removed = [&](uint64_t c_incl, float p) {
         return D::rn(D::rn(static_cast<float>(from_fx(c_incl))) - p) >= t;
       };
+      const int lim = min(hi, L);
       uint64_t local = 0;
-      for (int i = lo; i < min(hi, L); ++i) local += ent_cnt(i) * to_fx(D::rn(E(i) * r1));
-      uint64_t tot;
-      const uint64_t base = block_excl_scan<uint64_t>(local, sh.redq, &tot);
-      int first = L;
       {
-        uint64_t c = base;
-        for (int i = lo; i < min(hi, L); ++i) {
-          const float p = D::rn(E(i) * r1);
-          const uint64_t pf = to_fx(p);
-          if (removed(c + pf, p)) { first = i; break; }
-          c += ent_cnt(i) * pf;
+        for (int i = lo; i < lim; ++i) local += cnt_of(i) * pf(i);
+      }
+      uint64_t tot;
+      const uint64_t sb = block_excl_scan<uint64_t>(local, sh.redq, &tot);
+      SliceX[tid] = sb;
+      if (cum_ok) {
+        uint64_t c = sb;
+        for (int i = lo; i < lim; ++i) {
+          CumX[i] = c;
+          c += cnt_of(i) * pf(i);
         }
       }
-      const int i1 = block_reduce<int32_t>(first, OpMin(), sh.redi);
-      if (i1 == 0) {
-        status |= FL_ROW_ALL_MASKED;
-      } else if (i1 < L) {
-        i0 = i1 - 1;
-        if (i0 >= lo && i0 < hi) {
-          uint64_t c = base;
-          for (int i = lo; i < i0; ++i) c += ent_cnt(i) * to_fx(D::rn(E(i) * r1));
+      __syncthreads();
+      if (w0) {
+        auto cx = [&](int i) -> uint64_t {  // p-mass before entry i (exact fixed point)
+          if (cum_ok) return CumX[i];
+          const int s = i / per;
+          uint64_t c = SliceX[s];
+          for (int j = s * per; j < i; ++j) c += cnt_of(j) * pf(j);
+          return c;
+        };
+        const int i1 = wave_first(0, L, [&](int i) { return removed(cx(i) + pf(i), D::rn(E(i) * r1)); });
+        int i0 = L - 1;
+        uint32_t c0 = cnt_of(L - 1);
+        if (i1 == 0) {
+          i0 = -1;
+        } else if (i1 < L) {
+          i0 = i1 - 1;
+          const uint64_t c = cx(i0);
           const float p = D::rn(E(i0) * r1);
-          const uint64_t pf = to_fx(p);
-          const uint32_t n = ent_cnt(i0);
-          // members [0, kept) survive; member 0 is known to survive
-          uint32_t klo = 1, khi = n;  // answer in [klo, khi]
-          while (klo < khi) {
-            const uint32_t mid = (klo + khi + 1) >> 1;   // does member mid-1 survive?
-            if (!removed(c + static_cast<uint64_t>(mid) * pf, p)) klo = mid;
-            else khi = mid - 1;
-          }
-          sh.c0 = klo;
+          const uint64_t pfi = to_fx(p);
+          // member j of entry i0 is removed iff removed(c + (j+1) pf, p);
+          // member 0 is known to survive
+          c0 = static_cast<uint32_t>(wave_first(1, static_cast<int>(cnt_of(i0)), [&](int j) {
+            return removed(c + static_cast<uint64_t>(j + 1) * pfi, p);
+          }));
         }
-        __syncthreads();
-        c0 = sh.c0;
-      }
-    }
-  }
-
-  if (status == 0) {
-    // ---------------- group of the last kept entry
-    const float ycut = Y(i0);
-    cut_lo = i0;
-    while (cut_lo > 0 && Y(cut_lo - 1) == ycut) --cut_lo;
-    cut_hi = i0;
-    while (cut_hi + 1 < N && Y(cut_hi + 1) == ycut) ++cut_hi;
-    for (int i = cut_lo; i <= cut_hi; ++i) {
-      cut_total += ent_cnt(i);
-      if (i < i0) cut_kept += ent_cnt(i);
-    }
-    cut_kept += c0;
-
-    auto kc = [&](int i) -> uint32_t { return i < i0 ? ent_cnt(i) : (i == i0 ? c0 : 0u); };
-
-    // ---------------- softmax of the filtered row (sampling.py:58)
-    {
-      double s = 0.0;
-      uint32_t n = 0;
-      for (int i = lo; i < min(hi, i0 + 1); ++i) {
-        s += static_cast<double>(kc(i)) * E(i);
-        n += kc(i);
-      }
-      SK = block_reduce<double>(s, OpAdd(), sh.redd);
-      n_kept = block_reduce<uint32_t>(n, OpAdd(), sh.redu);
-    }
-    rK = 1.0f / static_cast<float>(SK);
-
-    if (select) {
-      if (T <= 0.0f) {
-        // greedy (sampling.py:59-60): first index among the maximal probabilities
-        const float qmax = D::rn(E(0) * rK);
-        int last = 0;
-        for (int i = lo; i < min(hi, i0 + 1); ++i)
-          if (D::rn(E(i) * rK) == qmax) last = i;
-        last = block_reduce<int32_t>(last, OpMax(), sh.redi);
-        sel_lo = 0;
-        sel_hi = last;
-        const float yl = Y(last);
-        while (sel_hi + 1 < N && Y(sel_hi + 1) == yl) ++sel_hi;
-        sel_rank = 0;
-      } else {
-        // inverse CDF (CONVENTION replacing torch.multinomial, sampling.py:61):
-        // first member whose inclusive cumulative probability exceeds u * total,
-        // cumulative sums in exact 2^-46 fixed point
-        uint64_t local = 0;
-        for (int i = lo; i < min(hi, i0 + 1); ++i) local += kc(i) * to_fx(D::rn(E(i) * rK));
-        uint64_t Q;
-        const uint64_t base = block_excl_scan<uint64_t>(local, sh.redq, &Q);
-        const uint64_t target = __double2ull_rd(static_cast<double>(U) * static_cast<double>(Q));
         if (tid == 0) {
-          sh.sel_entry = -1;
-          sh.sel_cexcl = 0;
+          sh.dec.i0 = i0;
+          sh.dec.c0 = c0;
         }
-        __syncthreads();
-        {
-          uint64_t c = base;
-          for (int i = lo; i < min(hi, i0 + 1); ++i) {
-            const uint64_t m = kc(i) * to_fx(D::rn(E(i) * rK));
-            if (m > 0 && c <= target && target < c + m) sh.sel_entry = i;
-            c += m;
-          }
-        }
-        __syncthreads();
-        int is = sh.sel_entry;
-        if (is < 0) {
-          // no positive mass at all (every kept probability rounds to zero)
-          is = 0;
-        }
-        const float ys = Y(is);
-        sel_lo = is;
-        while (sel_lo > 0 && Y(sel_lo - 1) == ys) --sel_lo;
-        sel_hi = is;
-        while (sel_hi + 1 < N && Y(sel_hi + 1) == ys) ++sel_hi;
-        // cumulative mass before the selected value group
-        {
-          uint64_t c = base;
-          for (int i = lo; i < min(hi, i0 + 1); ++i) {
-            if (i == sel_lo) sh.sel_cexcl = c;
-            c += kc(i) * to_fx(D::rn(E(i) * rK));
-          }
-        }
-        __syncthreads();
-        const uint64_t cg = sh.sel_cexcl;
-        const uint64_t q = to_fx(D::rn(E(is) * rK));
-        uint32_t kept_g = 0;
-        for (int i = sel_lo; i <= sel_hi; ++i) kept_g += kc(i);
-        // member r of the group covers [cg + r q, cg + (r+1) q)
-        uint64_t r = (q > 0 && target >= cg) ? (target - cg) / q : 0;
-        sel_rank = static_cast<uint32_t>(min(r, static_cast<uint64_t>(kept_g - 1)));
+      }
+    } else if (tid == 0) {
+      sh.dec.i0 = L - 1;
+      sh.dec.c0 = cnt_of(L - 1);
+    }
+    __syncthreads();
+  }
+  FL_MARK(15);
+
+  // ---------------- cut group, softmax (:58) and selection (:59-61)
+  int i0 = sh.dec.i0;
+  uint32_t c0 = sh.dec.c0;
+  if (status == 0 && i0 < 0) status |= FL_ROW_ALL_MASKED;
+  if (status == 0) {
+    if (w0) {
+      const float ycut = Y(i0);
+      const int cut_lo = wave_first(0, i0 + 1, [&](int i) { return Y(i) <= ycut; });
+      const int cut_hi = wave_first(i0 + 1, N, [&](int i) { return Y(i) < ycut; }) - 1;
+      const uint32_t n_before_i0 = count_before(i0);
+      const uint32_t n_before_lo = count_before(cut_lo);
+      const double SK = from_fx(mass_before(i0) + c0 * to_fx(E(i0)));
+      if (tid == 0) {
+        sh.dec.cut_total = count_before(cut_hi + 1) - n_before_lo;
+        sh.dec.cut_kept = n_before_i0 - n_before_lo + c0;
+        sh.dec.cut_lo = cut_lo;
+        sh.dec.cut_hi = cut_hi;
+        sh.dec.n_kept = n_before_i0 + c0;
+        sh.dec.SK = SK;
+        sh.dec.y_cut = ycut;
       }
     }
+    __syncthreads();
   }
-  // values the output stage needs, read before the entry list is overwritten
-  const float y_sel = (status == 0 && select) ? Y(sel_lo) : 0.0f;
-  const float y_cut = (status == 0) ? Y(i0) : __builtin_inff();
-  __syncthreads();
+  const double SK = sh.dec.SK;
+  const float rK = 1.0f / static_cast<float>(SK);
+  const uint32_t n_kept = sh.dec.n_kept;
+  auto kc = [&](int i) -> uint32_t { return i < i0 ? cnt_of(i) : (i == i0 ? c0 : 0u); };
+  auto kept_before = [&](int Lb) -> uint32_t { return Lb <= i0 ? count_before(Lb) : n_kept; };
+  if (status == 0 && select) {
+    if (T <= 0.0f) {
+      // greedy (sampling.py:59-60): first index among the maximal probabilities
+      if (w0) {
+        const float qmax = D::rn(E(0) * rK);
+        const int last = wave_first(1, i0 + 1, [&](int i) { return D::rn(E(i) * rK) != qmax; }) - 1;
+        const float yl = Y(last);
+        const int sh_hi = wave_first(last + 1, N, [&](int i) { return Y(i) < yl; }) - 1;
+        if (tid == 0) {
+          sh.dec.sel_lo = 0;
+          sh.dec.sel_hi = sh_hi;
+          sh.dec.sel_rank = 0;
+          sh.dec.y_sel = Y(0);
+        }
+      }
+    } else {
+      // inverse CDF (CONVENTION replacing torch.multinomial, sampling.py:61):
+      // first member whose inclusive cumulative probability exceeds u * total,
+      // cumulative sums in exact 2^-46 fixed point
+      auto qf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * rK)); };
+      const int lim = min(hi, i0 + 1);
+      uint64_t local = 0;
+      {
+        for (int i = lo; i < lim; ++i) local += kc(i) * qf(i);
+      }
+      uint64_t Q;
+      const uint64_t sb = block_excl_scan<uint64_t>(local, sh.redq, &Q);
+      SliceX[tid] = sb;
+      if (cum_ok) {
+        uint64_t c = sb;
+        for (int i = lo; i < lim; ++i) {
+          CumX[i] = c;
+          c += kc(i) * qf(i);
+        }
+      }
+      __syncthreads();
+      if (w0) {
+        auto cq = [&](int i) -> uint64_t {  // q-mass before entry i
+          if (cum_ok) return CumX[i];
+          const int s = i / per;
+          uint64_t c = SliceX[s];
+          for (int j = s * per; j < i; ++j) c += kc(j) * qf(j);
+          return c;
+        };
+        const uint64_t target = __double2ull_rd(static_cast<double>(U) * static_cast<double>(Q));
+        int is = wave_first(0, i0 + 1, [&](int i) { return cq(i) + kc(i) * qf(i) > target; });
+        if (is > i0) is = 0;  // no positive mass at all (every kept probability rounds to zero)
+        const float ys = Y(is);
+        const int s_lo = wave_first(0, is + 1, [&](int i) { return Y(i) <= ys; });
+        const int s_hi = wave_first(is + 1, N, [&](int i) { return Y(i) < ys; }) - 1;
+        const uint64_t cg = cq(s_lo);
+        const uint64_t q = qf(is);
+        const uint32_t kept_g = kept_before(s_hi + 1) - kept_before(s_lo);
+        // member r of the group covers [cg + r q, cg + (r+1) q)
+        const uint64_t r = (q > 0 && target >= cg) ? (target - cg) / q : 0;
+        if (tid == 0) {
+          sh.dec.sel_lo = s_lo;
+          sh.dec.sel_hi = s_hi;
+          sh.dec.sel_rank = static_cast<uint32_t>(min(r, static_cast<uint64_t>(kept_g > 0 ? kept_g - 1 : 0)));
+          sh.dec.y_sel = ys;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int cut_lo = sh.dec.cut_lo, cut_hi = sh.dec.cut_hi;
+  const uint32_t cut_kept = sh.dec.cut_kept, cut_total = sh.dec.cut_total;
+  const int sel_lo = sh.dec.sel_lo, sel_hi = sh.dec.sel_hi;
+  const uint32_t sel_rank = sh.dec.sel_rank;
+  const float y_sel = sh.dec.y_sel;
+  const float y_cut = status == 0 ? sh.dec.y_cut : __builtin_inff();
   FL_MARK(6);
 
   // ------------------------------------------------ identification
@@ -602,19 +663,6 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
       }
     }
-    // Packed 16-bit range test of both halves of a word: a wrapping subtract
-    // of the range start, then a saturating subtract of the width, leaves 0
-    // exactly in the halves inside the range.
-    auto range_test = [&](uint32_t w, int r) -> uint32_t {
-      const u16x2 d = __builtin_bit_cast(u16x2, w) - u16x2{static_cast<unsigned short>(rlo[r]),
-                                                            static_cast<unsigned short>(rlo[r])};
-      return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(
-                                              d, u16x2{static_cast<unsigned short>(rw[r]),
-                                                       static_cast<unsigned short>(rw[r])}));
-    };
-    // non-zero iff a half of e is zero (may also flag a half above a zero
-    // one; the exact test on the hit path sorts that out)
-    auto zero_halves = [](uint32_t e) { return (e - 0x00010001u) & ~e & 0x80008000u; };
     auto candidate = [&](int idx, int t) {
       if (idx < V && !is_hist(idx)) {
         const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
@@ -635,49 +683,68 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     const int nchunks = (V + 7) >> 3;
     if (fast) {
       // Non-history elements whose value lies in a target group.  The row is
-      // read again, all chunks in flight at once (mostly a cache hit); each
-      // chunk gets a branch-free packed test, and the rare hit chunks are
-      // queued in LDS and examined element by element afterwards, which keeps
-      // this loop small enough to stay unrolled with the tile in VGPRs.
+      // read again (mostly a cache hit: keeping the VGPR tile through the
+      // decisions would spill), each chunk gets a branch-free packed test, and
+      // the rare hit chunks are queued in LDS with their data, to be examined
+      // element by element by all threads afterwards.
       uint4 r[NCH];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) r[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
       FL_MARK(13);
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        uint32_t any = 0;
+        // packed (w - lo) per half, minimum over the chunk's 8 elements: a
+        // chunk holds a member of range rr iff that minimum is <= width
+        bool hit = false;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           if (!ren[rr]) continue;  // wave-uniform
-          any |= zero_halves(range_test(r[j].x, rr)) | zero_halves(range_test(r[j].y, rr)) |
-                 zero_halves(range_test(r[j].z, rr)) | zero_halves(range_test(r[j].w, rr));
+          const unsigned short l16 = static_cast<unsigned short>(rlo[rr]);
+          const u16x2 lo2 = {l16, l16};
+          const u16x2 m = __builtin_elementwise_min(
+              __builtin_elementwise_min(__builtin_bit_cast(u16x2, r[j].x) - lo2, __builtin_bit_cast(u16x2, r[j].y) - lo2),
+              __builtin_elementwise_min(__builtin_bit_cast(u16x2, r[j].z) - lo2, __builtin_bit_cast(u16x2, r[j].w) - lo2));
+          hit |= min(static_cast<uint32_t>(m[0]), static_cast<uint32_t>(m[1])) <= rw[rr];
         }
         const int c = j * NT + tid;
-        if (any != 0 && c < nchunks) {
+        if (hit && c < nchunks) {
           const uint32_t s = atomicAdd(&sh.nhit, 1u);
-          if (s < static_cast<uint32_t>(HIT_CAP)) hitq[s] = c;
+          if (s < static_cast<uint32_t>(HIT_CAP)) {
+            hitq[5 * s] = c;
+            hitq[5 * s + 1] = r[j].x;
+            hitq[5 * s + 2] = r[j].y;
+            hitq[5 * s + 3] = r[j].z;
+            hitq[5 * s + 4] = r[j].w;
+          }
         }
       }
       FL_MARK(14);
       __syncthreads();
+    }
+    {
+      // the queued chunks, or every chunk when the queue overflowed or the
+      // row is not in the VGPR tile
       const uint32_t nhit = sh.nhit;
-      if (nhit <= static_cast<uint32_t>(HIT_CAP)) {
-        for (int i = tid; i < static_cast<int>(nhit); i += NT) {
-          const int c = hitq[i];
-          chunk_candidates(c, buf_load16(rrow, 16u * c, 0u));
+      const bool use_queue = fast && nhit <= static_cast<uint32_t>(HIT_CAP);
+      const int n_iter = use_queue ? static_cast<int>(nhit) : nchunks;
+      for (int i = tid; i < n_iter; i += NT) {
+        int c = i;
+        uint4 q;
+        if (use_queue) {
+          c = static_cast<int>(hitq[5 * i]);
+          q = make_uint4(hitq[5 * i + 1], hitq[5 * i + 2], hitq[5 * i + 3], hitq[5 * i + 4]);
+        } else {
+          q = fast ? buf_load16(rrow, 16u * c, 0u) : load_chunk16(row, c, V, ALIGNED);
         }
-      } else {
-        for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, buf_load16(rrow, 16u * c, 0u));
+        chunk_candidates(c, q);
       }
-    } else {
-      for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, load_chunk16(row, c, V, ALIGNED));
     }
     // history elements whose penalised value lies in a target group (the
     // first HPRE ids of each thread and their logits are still in registers)
     if (pen) {
       auto hist_candidate = [&](int id, uint32_t raw) {
         const uint32_t z = elem_bits(raw);
-        const uint32_t zp = D::from_f32(penalty_val<D>(D::to_f32(z), RP));
+        const uint32_t zp = penalised_bits<D>(z, RP);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if (active[t] && in_range(t, zp)) {
@@ -697,21 +764,65 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     __syncthreads();
     FL_MARK(7);
+    // The member of rank r (by index) among a target's candidates: bucket
+    // counts over 128-index buckets locate the bucket holding rank r, and a
+    // 128-bit mask of that bucket's members gives the index.
+    uint32_t* bins = sh.hist + 2 * LIST_CAP;  // the hit queue is no longer needed
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
       const int n = static_cast<int>(sh.nlist[t]);
-      if (n <= RANK_SELECT_MAX) {
-        // rank by all-pairs counting over the (distinct) candidate indices
+      if (n <= LIST_CAP) {
+        for (int i = tid; i < RANK_BINS + 4; i += NT) bins[i] = 0;
+        if (tid == 0) sh.rank_bin = 0xFFFFFFFFu;
+        __syncthreads();
+        for (int i = tid; i < n; i += NT) atomicAdd(&bins[list[t][i] >> 7], 1u);
+        __syncthreads();
+        if (tid < WAVE) {
+          // wave 0: running counts over the buckets, 16 per lane
+          constexpr int PER = RANK_BINS / WAVE;
+          uint32_t c = 0;
+#pragma unroll
+          for (int k = 0; k < PER; ++k) c += bins[tid * PER + k];
+          const uint32_t incl = wave_incl_scan(c);
+          const uint32_t excl = incl - c;
+          if (excl <= rank[t] && rank[t] < incl) {
+            uint32_t run = excl;
+            for (int k = 0; k < PER; ++k) {
+              const uint32_t bk = bins[tid * PER + k];
+              if (rank[t] < run + bk) {
+                sh.rank_bin = tid * PER + k;
+                sh.rank_in_bin = rank[t] - run;
+                break;
+              }
+              run += bk;
+            }
+          }
+        }
+        __syncthreads();
+        const uint32_t rb = sh.rank_bin;
+        uint32_t* mask = bins + RANK_BINS;  // 128 bits
         for (int i = tid; i < n; i += NT) {
           const uint32_t v = list[t][i];
-          uint32_t below = 0;
-          for (int k2 = 0; k2 < n; ++k2) below += list[t][k2] < v;
-          if (below == rank[t]) sh.result[t] = static_cast<int32_t>(v);
+          if ((v >> 7) == rb) atomicOr(&mask[(v >> 5) & 3u], 1u << (v & 31u));
+        }
+        __syncthreads();
+        if (tid == 0) {
+          uint32_t need = sh.rank_in_bin;
+          for (int k = 0; k < 4; ++k) {
+            uint32_t m = mask[k];
+            const uint32_t pc = static_cast<uint32_t>(__popc(m));
+            if (need < pc) {
+              for (uint32_t q = 0; q < need; ++q) m &= m - 1u;  // drop the lowest `need` bits
+              sh.result[t] = static_cast<int32_t>(rb * 128u + 32u * k + (__ffs(m) - 1));
+              break;
+            }
+            need -= pc;
+          }
         }
       } else {
-        // too many candidates: count matches round by round in index order
-        // (re-reads the row from memory; a rare path kept out of the VGPR tile)
+        // the candidate list overflowed: count matches round by round in
+        // index order (re-reads the row from memory; a rare path)
         uint32_t base = 0;
         for (int j = 0; j < NCH; ++j) {
           const int e0 = (j * NT + tid) * 8;
@@ -720,7 +831,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
             const int idx = e0 + e;
             if (idx >= V) continue;
             uint32_t bits = elem_bits(row[idx]);
-            if (is_hist(idx)) bits = D::from_f32(penalty_val<D>(D::to_f32(bits), RP));
+            if (is_hist(idx)) bits = penalised_bits<D>(bits, RP);
             m |= static_cast<uint32_t>(in_range(t, bits)) << e;
           }
           uint32_t tot;
@@ -801,7 +912,8 @@ hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s) {
 #ifdef FL_PHASE_TIMES
 // Tuning builds only: copy the phase timestamps recorded by the last launch.
 extern "C" int fl_debug_phase_ts(uint64_t* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * 192, 0, hipMemcpyDeviceToHost) ==
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * (192 + 2048), 0,
+                             hipMemcpyDeviceToHost) ==
                  hipSuccess ? 0 : -1;
 }
 #endif
