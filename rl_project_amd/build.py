@@ -24,11 +24,15 @@ LIB_PATH = os.path.join(LIB_DIR, "libflsampler.so")
 ARCH = os.environ.get("FL_OFFLOAD_ARCH", "gfx950")
 
 # Correctly rounded float32 division (the reference's x / T is IEEE division),
-# IEEE denormals (PyTorch's CPU kernels keep them), no packed-fp32 ops.
+# IEEE denormals (PyTorch's CPU kernels keep them), no packed-fp32 ops.  The
+# scheduler's AMDGPU register-pressure trackers let the 16-bit row kernels
+# keep their 64-VGPR row tile from the first read to the last use without
+# spilling (the generic trackers misjudge the pressure and spill it).
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-use-amdgpu-trackers",
     "-mcode-object-version=5", "-Wall", "-Wno-unused-result",
 ]
 

@@ -129,15 +129,16 @@ __device__ __forceinline__ float temperature_val(float x, float t) {
 constexpr double FX_ONE = 70368744177664.0;  // 2^46
 // round(p * 2^46) for p in [0, 1] from the float's fields (ties round up);
 // integer arithmetic only
+// (branch-free: with m = the 24-bit significand, p * 2^46 = m * 2^(ex - 104)
+// = (m << 24) >> (128 - ex); a right shift of 49 or more leaves 0, as do
+// zero and denormals)
 __device__ __forceinline__ uint64_t to_fx(float p) {
   const uint32_t u = __float_as_uint(p);
-  const int ex = static_cast<int>(u >> 23);
-  if (ex == 0) return 0;  // zero or denormal (< 2^-126): below the resolution
-  const uint64_t m = (u & 0x7FFFFFu) | 0x800000u;  // p = m * 2^(ex - 150)
-  const int s = ex - 150 + 46;
-  if (s >= 0) return m << s;
-  if (s < -24) return 0;
-  return (m + (1ull << (-s - 1))) >> (-s);
+  const uint32_t ex = u >> 23;
+  const uint64_t m24 = static_cast<uint64_t>((u & 0x7FFFFFu) | 0x800000u) << 24;
+  const uint32_t sh = min(128u - ex, 63u);  // ex <= 127 for p <= 1 (p > 1 handled below)
+  const uint64_t r = (m24 + (1ull << (sh - 1))) >> sh;
+  return ex > 127u ? (m24 >> 24) << min(ex - 104u, 63u) : r;
 }
 __device__ __forceinline__ double from_fx(uint64_t v) { return static_cast<double>(v) * (1.0 / FX_ONE); }
 
@@ -179,33 +180,72 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return out;
 }
 
+// Integer inclusive scans on DPP alone (few temporaries): within each row of
+// 16 lanes, adds of the value 1, 2, 4 and 8 lanes down (row_shr); then
+// row_bcast:15 carries each row's total into the next row and row_bcast:31
+// the first two rows' total into the last two.  A lane whose source is out of
+// its row, or whose row is masked off, adds 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_or_zero64(uint64_t v) {
+  const uint32_t lo = dpp_or_zero<CTRL, ROW_MASK>(static_cast<uint32_t>(v));
+  const uint32_t hi = dpp_or_zero<CTRL, ROW_MASK>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_or_zero<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_or_zero<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_or_zero<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_or_zero<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_or_zero<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_or_zero<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
+  v += dpp_or_zero64<0x111, 0xF>(v);
+  v += dpp_or_zero64<0x112, 0xF>(v);
+  v += dpp_or_zero64<0x114, 0xF>(v);
+  v += dpp_or_zero64<0x118, 0xF>(v);
+  v += dpp_or_zero64<0x142, 0xA>(v);
+  v += dpp_or_zero64<0x143, 0xC>(v);
+  return v;
+}
+
 // Block-wide reduction in a fixed order (deterministic for floating point).
-// `red` holds NWAVE elements of T.  Contains two barriers.
-template <typename T, class Op>
+// `red` holds NW elements of T (NW = waves per work-group).  Two barriers.
+template <typename T, class Op, int NW = NWAVE>
 __device__ __forceinline__ T block_reduce(T v, Op op, T* red) {
   v = wave_reduce(v, op);
   if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
   __syncthreads();
   T r = red[0];
 #pragma unroll
-  for (int i = 1; i < NWAVE; ++i) r = op(r, red[i]);
+  for (int i = 1; i < NW; ++i) r = op(r, red[i]);
   __syncthreads();
   return r;
 }
 
 // Block-wide exclusive prefix sum in thread order; *total receives the sum.
-template <typename T>
+template <typename T, int NW = NWAVE>
 __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int w = threadIdx.x / WAVE;
   const T inc = wave_incl_scan(v);
-  T exc = shfl_up(inc, 1);
-  if (lane == 0) exc = T(0);
+  T exc;
+  if constexpr (__is_integral(T)) {
+    exc = inc - v;
+  } else {
+    exc = shfl_up(inc, 1);
+    if (lane == 0) exc = T(0);
+  }
   if (lane == WAVE - 1) red[w] = inc;
   __syncthreads();
   T base = T(0), tot = T(0);
 #pragma unroll
-  for (int i = 0; i < NWAVE; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const T x = red[i];
     if (i < w) base = base + x;
     tot = tot + x;
@@ -217,18 +257,15 @@ __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
 
 // Exclusive prefix sums of two quantities in thread order with one pair of
 // barriers; ta / tb receive the totals.
+template <int NW = NWAVE>
 __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_t* ra, uint64_t* rb, uint32_t& ea,
                                                  uint64_t& eb, uint32_t& ta, uint64_t& tb) {
   const int lane = threadIdx.x & (WAVE - 1);
   const int w = threadIdx.x / WAVE;
   const uint32_t ia = wave_incl_scan(a);
   const uint64_t ib = wave_incl_scan(b);
-  uint32_t xa = shfl_up(ia, 1);
-  uint64_t xb = shfl_up(ib, 1);
-  if (lane == 0) {
-    xa = 0;
-    xb = 0;
-  }
+  const uint32_t xa = ia - a;
+  const uint64_t xb = ib - b;
   if (lane == WAVE - 1) {
     ra[w] = ia;
     rb[w] = ib;
@@ -237,7 +274,7 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_
   uint32_t ba = 0, sa = 0;
   uint64_t bb = 0, sb = 0;
 #pragma unroll
-  for (int i = 0; i < NWAVE; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint32_t x = ra[i];
     const uint64_t y = rb[i];
     if (i < w) {

@@ -32,16 +32,12 @@ constexpr int HIST_WORDS = 32768;                // 65536 packed u16 counters
 constexpr int HBITS_WORDS = FL_MAX_VOCAB_16 / 32;
 constexpr int OWNER_WORDS = FL_MAX_HISTORY / 32;
 constexpr int LIST_CAP = HIST_WORDS / 4;          // candidates per identification target
-constexpr int HIT_CAP = (HIST_WORDS / 2) / 5;     // queued chunks (index + 4 data words), after the lists
 constexpr int RANK_BINS = FL_MAX_VOCAB_16 / 128;  // index buckets of the rank selection
-constexpr int SLICE_BASE = HIST_WORDS - 5 * NT;   // slice tables: count u32[NT], mass u64[NT], scan u64[NT]
+constexpr int SLICE_BASE = HIST_WORDS - 3 * NT;   // slice tables: count u32[NT], mass u64[NT]
 constexpr int ENT_MAX = SLICE_BASE;               // entries (distinct values) a row may have
-constexpr int YE_CACHE_MAX = ENT_MAX / 3;         // entries whose y and e are kept beside them
-constexpr int CUM_MAX = ENT_MAX / 5 - 1;          // ... and also a 64-bit cumulative per entry
-constexpr int CUM_PER = 8;                        // most entries per thread with the cumulative kept
-// order block (4096 orders) handled by each wave: the blocks real logits
-// populate go to waves on different SIMDs (wave w runs on SIMD w % 4)
-__constant__ const int kBlockOfWave[16] = {3, 4, 11, 12, 5, 13, 0, 1, 2, 6, 7, 8, 9, 10, 14, 15};
+constexpr int CACHE_MAX = (SLICE_BASE - 4) / 6;   // entries with y, e, prefix count and mass kept per entry
+constexpr int NSTEP = 512;                        // compaction steps of 128 orders
+constexpr int SPW = NSTEP / NWAVE;                // steps per wave
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 
 static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
@@ -52,20 +48,90 @@ struct Shared16 {
   uint32_t owner[OWNER_WORDS];
   uint64_t redq[NWAVE];
   uint32_t redu[NWAVE];
+  uint64_t scan_sum[NWAVE];
+  uint64_t scan_excl[NWAVE];
+  int32_t scan_idx[NWAVE];
+  alignas(16) uint32_t stepc[NSTEP];
   int32_t status;
   int32_t result[2];
   struct {
     double S, SK;
     int32_t L, i0, cut_lo, cut_hi, sel_lo, sel_hi;
     uint32_t c0, cut_kept, cut_total, n_kept, sel_rank;
+    uint32_t o_lo[2], o_hi[2];
     float y_sel, y_cut;
-  } dec;  // decisions of the search wave
+  } dec;  // results of the search wave
   uint32_t nlist[2];
-  uint32_t nhit;
   uint32_t rank_bin, rank_in_bin;
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int NO_HIT = 0x7FFFFFFF;
+
+struct ScanHit {
+  int idx;         // first index whose predicate holds (n when none does)
+  uint64_t excl;   // sum of the terms before idx
+  uint64_t total;  // sum of all terms (or the total passed in)
+};
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Block-wide search along n terms in index order: the first i for which
+// pred(i, excl_i, total) holds, excl_i being the sum of the terms before i
+// (the predicate must be false, then true, along the indices).  The terms are
+// taken NT per round, one per thread; a round is a block scan with two
+// barriers, and the search stops at the first round with a hit.  `total` is
+// the sum of all n terms: known within the round when n <= NT, else passed in
+// (total_given).  Every thread of the block calls it with the same arguments.
+template <class TermF, class PredF>
+__device__ __forceinline__ ScanHit scan_first(Shared16& sh, int n, bool total_given, uint64_t total_in, TermF&& term,
+                                              PredF&& pred) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / WAVE);
+  uint64_t carry = 0;
+  for (int base = 0; base < n; base += NT) {
+    const int i = base + static_cast<int>(threadIdx.x);
+    const bool act = base + w * WAVE < n;  // wave-uniform: this wave holds terms this round
+    uint64_t v = 0, inc = 0;
+    if (act) {
+      v = i < n ? term(i) : 0ull;
+      inc = wave_incl_scan(v);
+    }
+    if (lane == WAVE - 1) sh.scan_sum[w] = inc;
+    lds_barrier();
+    const uint64_t wi = wave_incl_scan(lane < NWAVE ? sh.scan_sum[lane] : 0ull);
+    const uint64_t rtot = readlane64(wi, NWAVE - 1);
+    const uint64_t total = total_given ? total_in : carry + rtot;
+    int first = NO_HIT;
+    uint64_t fex = 0;
+    if (act) {
+      const uint64_t excl = carry + (w > 0 ? readlane64(wi, w - 1) : 0ull) + (inc - v);
+      const uint64_t m = __ballot(i < n && pred(i, excl, total));
+      if (m) {
+        const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        first = base + w * WAVE + f;
+        fex = readlane64(excl, f);
+      }
+    }
+    if (lane == 0) {
+      sh.scan_idx[w] = first;
+      sh.scan_excl[w] = fex;
+    }
+    lds_barrier();
+    const uint64_t hm = __ballot(lane < NWAVE && sh.scan_idx[lane] != NO_HIT);
+    carry += rtot;
+    if (hm) {
+      const int fw = __ffsll(static_cast<unsigned long long>(hm)) - 1;
+      return {sh.scan_idx[fw], sh.scan_excl[fw], total};
+    }
+  }
+  return {n, carry, total_given ? total_in : carry};
+}
 
 // 16-byte chunk c (elements 8c .. 8c+7) of a row; elements >= V read as 0.
 __device__ __forceinline__ uint4 load_chunk16(const uint16_t* row, int c, int V, bool aligned) {
@@ -104,17 +170,34 @@ template <class D>
 __device__ __noinline__ float e_of_order(uint32_t order, float cap, float t, bool sc, float M) {
   return expf(value_of_order<D>(order, cap, t, sc) - M);
 }
+// The same for a kernel instantiated with or without the soft-cap: without
+// it the value is cheap and inline, and the kernel makes no calls (a call
+// would keep most VGPRs from holding values across it).
+template <class D, bool SC>
+__device__ __forceinline__ float y_of_order(uint32_t order, float cap, float t, bool sc) {
+  if constexpr (SC) return value_of_order<D>(order, cap, t, sc);
+  else return temperature_val<D>(D::to_f32(bits_of_order16(order)), t);
+}
+template <class D, bool SC>
+__device__ __forceinline__ float exp_of_order(uint32_t order, float cap, float t, bool sc, float M) {
+  if constexpr (SC) return e_of_order<D>(order, cap, t, sc, M);
+  else return expf(y_of_order<D, false>(order, cap, t, false) - M);
+}
 
 }  // namespace
 
-template <class D>
-__global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM) {
+// SC: the row has a soft-cap (applied per element when SC_ELEM, else per
+// entry).  The instantiation without it keeps the first read's VGPR tile for
+// the identification; the one with it reads the row again.
+template <class D, bool SC>
+__global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN) {
   __shared__ Shared16 sh;
   FL_MARK(0);
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int V = static_cast<int>(a.vocab);
   const uint16_t* row = static_cast<const uint16_t*>(a.logits) + b * a.ld;
+  const bool SC_ELEM = SC && SC_ELEM_IN;
   const int nfull = V >> 3;                               // chunks holding 8 valid elements
   const bool fast = ALIGNED && !SC_ELEM && nfull > 0;     // whole row through the VGPR tile
 
@@ -158,7 +241,6 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   if (tid == 0) {
     sh.status = 0;
     sh.nlist[0] = sh.nlist[1] = 0;
-    sh.nhit = 0;
     sh.result[0] = sh.result[1] = -1;
     sh.dec.L = 0;
     sh.dec.i0 = -1;
@@ -167,6 +249,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     sh.dec.cut_lo = sh.dec.cut_hi = sh.dec.sel_lo = 0;
     sh.dec.sel_hi = -1;
     sh.dec.cut_kept = sh.dec.cut_total = sh.dec.n_kept = sh.dec.sel_rank = 0;
+    sh.dec.o_lo[0] = sh.dec.o_lo[1] = sh.dec.o_hi[0] = sh.dec.o_hi[1] = 0;
     sh.dec.y_sel = 0.0f;
     sh.dec.y_cut = __builtin_inff();
   }
@@ -178,9 +261,15 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // would also wait for the row on the path that loaded it; a row the fast
   // path does not take gets an empty range, so its loads return zeros)
   const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast ? 2u * static_cast<uint32_t>(V) : 0u);
+  // (issued in chunk order, pinned by scheduling barriers: the count pass
+  // takes the chunks in that order, and counting a chunk whose load was issued
+  // late would hold back the counting of all chunks after it)
   uint4 d[NCH];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+  for (int j = 0; j < NCH; ++j) {
+    d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // u outside [0, 1) (or NaN) is clamped into it
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
@@ -188,7 +277,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const bool hist_too_long = H_in > FL_MAX_HISTORY;
   const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
-  const bool sc_entry = (CAP > 0.0f) && !SC_ELEM;
+  const bool sc_entry = SC && (CAP > 0.0f) && !SC_ELEM;
   if (tid == 0 && hist_too_long) atomicOr(&sh.status, FL_ROW_LIMIT);
 
   // Value pattern of an element as the filters see it before penalty.
@@ -264,92 +353,100 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   FL_MARK(2);
 
   // ------------------------------------------------ compact to entries
-  // Order o = 0 is the largest value.  Wave w owns the 4096 orders of block
-  // kBlockOfWave[w]; in step i lane l reads the word of orders
-  // block*4096 + 128i + 2l and +1, so a wave's 64 reads hit 64 consecutive
-  // LDS words (no bank conflicts) and its entries for step i are consecutive
-  // (positions from ballots).  The permutation puts the blocks that real
-  // logits populate (|x| in about [2^-32, 2^32]: blocks 3-5 and 11-13) on
-  // different SIMDs.
+  // Order o = 0 is the largest value.  Step s covers orders 128s .. 128s+127
+  // (64 histogram words); wave w takes steps w, w + 16, ..., w + 496, so the
+  // few dozen consecutive steps that real logits populate are spread over all
+  // waves.  In a step, lane l reads the word of orders 128s + 2l and + 1: the
+  // 64 reads hit 64 consecutive words (no bank conflicts).  Entry counts per
+  // step go through LDS; each wave scans the 512 counts itself to place its
+  // steps' entries.
   int N;
   {
-    const int wave = tid / WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int lane = tid & (WAVE - 1);
-    const int blk = kBlockOfWave[wave];
-    const bool posb = blk < NWAVE / 2;  // positive values (wave-uniform)
-    const uint32_t ob = 4096u * blk;
-    uint32_t x[32];
+    uint32_t x[SPW];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      // word of orders ob + 128i + 2l (first half after the swap) and + 1
-      const int W = posb ? (0x3FFF - 2048 * blk - 64 * i - lane) : (2048 * blk + 64 * i + lane);
-      const uint32_t w = sh.hist[W];
-      x[i] = posb ? __builtin_amdgcn_alignbit(w, w, 16) : w;
+    for (int k = 0; k < SPW; ++k) {
+      const int s = wave + NWAVE * k;
+      if (k < SPW / 2) {
+        // positive values (s < 256): the word holds order o + 1 in its low
+        // half and o in its high half; swap so the low half is order o
+        const uint32_t w = sh.hist[0x3FFF - 64 * s - lane];
+        x[k] = __builtin_amdgcn_alignbit(w, w, 16);
+      } else {
+        x[k] = sh.hist[64 * s + lane];
+      }
     }
-    // NaN patterns occupy the two ends of the order (the first steps of block
-    // 0, the last steps of block 15): drop them, flag the row
+    // NaN patterns occupy the two ends of the order: the first NAN_STEPS
+    // steps (k = 0 of the first waves) and the last (k = SPW - 1 of the last
+    // waves).  Drop them and flag the row.
     constexpr int NAN_STEPS = (0x8000 - static_cast<int>(D::INF_BITS) + 127) / 128;
-    if (blk == 0 || blk == NWAVE - 1) {
-      bool nan = false;
+    static_assert(NAN_STEPS <= NWAVE, "NaN steps fit one step per wave");
+    bool nan = false;
+    if (wave < NAN_STEPS) {
+      const uint32_t o = 128u * wave + 2u * lane;
+      uint32_t keep = 0;
 #pragma unroll
-      for (int k = 0; k < NAN_STEPS; ++k) {
-        const int i = blk == 0 ? k : 31 - k;
-        uint32_t xi = x[0];
+      for (int h = 0; h < 2; ++h) keep |= (o + h < 0x7FFFu - D::INF_BITS) ? 0u : (h ? 0xFFFF0000u : 0x0000FFFFu);
+      nan |= (x[0] & ~keep) != 0u;
+      x[0] &= keep;
+    }
+    if (wave >= NWAVE - NAN_STEPS) {
+      const uint32_t o = 128u * (wave + NWAVE * (SPW - 1)) + 2u * lane;
+      uint32_t keep = 0;
 #pragma unroll
-        for (int j = 1; j < 32; ++j) xi = (j == i) ? x[j] : xi;  // static-index select
-        const uint32_t o = ob + 128u * i + 2u * lane;
-        uint32_t keep = 0;
+      for (int h = 0; h < 2; ++h) keep |= (o + h > 0x8000u + D::INF_BITS) ? 0u : (h ? 0xFFFF0000u : 0x0000FFFFu);
+      nan |= (x[SPW - 1] & ~keep) != 0u;
+      x[SPW - 1] &= keep;
+    }
+    if (nan) atomicOr(&sh.status, FL_ROW_NAN);
+    // entries of step wave + 16k, held by lane k
+    uint32_t cv = 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t oh = o + h;
-          const bool is_nan = posb ? (oh < 0x7FFFu - D::INF_BITS) : (oh > 0x8000u + D::INF_BITS);
-          keep |= is_nan ? 0u : (h ? 0xFFFF0000u : 0x0000FFFFu);
-        }
-        nan |= (xi & ~keep) != 0u;
-#pragma unroll
-        for (int j = 0; j < 32; ++j)
-          if (j == i) x[j] &= keep;
+    for (int k = 0; k < SPW; ++k) {
+      if (__ballot(x[k] != 0u) != 0) {
+        const uint32_t c = static_cast<uint32_t>(__popcll(__ballot((x[k] & 0xFFFFu) != 0u)) +
+                                                 __popcll(__ballot((x[k] >> 16) != 0u)));
+        cv = (lane == k) ? c : cv;
       }
-      if (nan) atomicOr(&sh.status, FL_ROW_NAN);
     }
-    uint32_t any = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) any |= x[i];
-    uint32_t wtot = 0;  // entries of this wave (wave-uniform)
-    if (__ballot(any != 0u) != 0) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i)
-        wtot += __popcll(__ballot((x[i] & 0xFFFFu) != 0u)) + __popcll(__ballot((x[i] >> 16) != 0u));
-    }
-    if (lane == 0) sh.redu[blk] = wtot;
+    if (lane < SPW) sh.stepc[wave + NWAVE * lane] = cv;
     __syncthreads();
-    uint32_t base = 0, tot = 0;
+    // lane l: the counts of steps 8l .. 8l+7.  This wave's steps sit at
+    // position wave % 8 of lanes 2k + wave / 8.
+    const uint4 s0 = reinterpret_cast<const uint4*>(sh.stepc)[2 * lane];
+    const uint4 s1 = reinterpret_cast<const uint4*>(sh.stepc)[2 * lane + 1];
+    const uint32_t sc8[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int jw = wave & 7;
+    uint32_t lsum = 0, pre = 0;
 #pragma unroll
-    for (int k = 0; k < NWAVE; ++k) {
-      const uint32_t t = sh.redu[k];
-      if (k < blk) base += t;
-      tot += t;
+    for (int j = 0; j < 8; ++j) {
+      pre += (j < jw) ? sc8[j] : 0u;
+      lsum += sc8[j];
     }
-    if (wtot) {
-      // branch-free: an empty half writes to this lane's spare slot past the
-      // entry area instead of being skipped
-      const uint32_t spare = ENT_MAX + 2u * lane;
+    const uint32_t linc = wave_incl_scan(lsum);
+    const uint32_t start = linc - lsum + pre;  // entries before step 8 * lane + wave % 8
+    const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(linc), WAVE - 1));
+    // branch-free within a step: an empty half writes to this lane's spare
+    // slot past the entry area instead of being skipped
+    const uint32_t spare = ENT_MAX + 2u * lane;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const uint32_t a1 = x[i] & 0xFFFFu, a2 = x[i] >> 16;
-        const uint64_t m1 = __ballot(a1 != 0u), m2 = __ballot(a2 != 0u);
-        const uint32_t below =
-            __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32),
-                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0)) +
-            __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32),
-                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
-        const uint32_t o = ob + 128u * i + 2u * lane;
-        const uint32_t p1 = base + below;
-        const uint32_t p2 = p1 + (a1 ? 1u : 0u);
-        sh.hist[(a1 && p1 < static_cast<uint32_t>(ENT_MAX)) ? p1 : spare] = (o << 16) | a1;
-        sh.hist[(a2 && p2 < static_cast<uint32_t>(ENT_MAX)) ? p2 : spare + 1u] = ((o + 1u) << 16) | a2;
-        base += static_cast<uint32_t>(__popcll(m1) + __popcll(m2));
-      }
+    for (int k = 0; k < SPW; ++k) {
+      const uint32_t a1 = x[k] & 0xFFFFu, a2 = x[k] >> 16;
+      const uint64_t m1 = __ballot(a1 != 0u), m2 = __ballot(a2 != 0u);
+      if ((m1 | m2) == 0) continue;
+      const uint32_t base =
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(start), 2 * k + (wave >> 3)));
+      const uint32_t below =
+          __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32),
+                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0)) +
+          __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32),
+                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
+      const uint32_t o = 128u * static_cast<uint32_t>(wave + NWAVE * k) + 2u * lane;
+      const uint32_t p1 = base + below;
+      const uint32_t p2 = p1 + (a1 ? 1u : 0u);
+      sh.hist[(a1 && p1 < static_cast<uint32_t>(ENT_MAX)) ? p1 : spare] = (o << 16) | a1;
+      sh.hist[(a2 && p2 < static_cast<uint32_t>(ENT_MAX)) ? p2 : spare + 1u] = ((o + 1u) << 16) | a2;
     }
     N = static_cast<int>(min(tot, static_cast<uint32_t>(ENT_MAX)));
     if (tid == 0 && tot > static_cast<uint32_t>(ENT_MAX)) atomicOr(&sh.status, FL_ROW_LIMIT);
@@ -359,44 +456,44 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 
   // ------------------------------------------------ entry values
   // Entry i: order ent[i] >> 16, count ent[i] & 0xFFFF, value Y(i) after
-  // soft-cap and temperature, E(i) = exp(Y(i) - M), cached beside the list
-  // when it fits.  Thread t owns the contiguous slice [t*per, t*per + per);
-  // the slice tables hold the count and the fixed-point mass before each
-  // slice, so any prefix sum is a table read plus fewer than `per` terms.
+  // soft-cap and temperature, E(i) = exp(Y(i) - M).  Thread t owns the
+  // contiguous slice [t*per, t*per + per).  When the row has at most
+  // CACHE_MAX entries, Y, E and the exclusive prefix counts and fixed-point
+  // masses are kept per entry (any prefix is one read); otherwise values are
+  // recomputed and prefixes are a slice-table read plus fewer than `per`
+  // terms.
   uint32_t* ent = sh.hist;
-  const bool cached = N <= YE_CACHE_MAX;
+  const bool cached = N <= CACHE_MAX;
   float* Yc = reinterpret_cast<float*>(sh.hist + N);
   float* Ec = reinterpret_cast<float*>(sh.hist + 2 * N);
+  uint32_t* Cc = sh.hist + 3 * N;                                         // N + 1 counts
+  uint64_t* Cm = reinterpret_cast<uint64_t*>(sh.hist + 4 * N + 2);        // N + 1 masses
   uint32_t* SliceCnt = sh.hist + SLICE_BASE;
   uint64_t* SliceM = reinterpret_cast<uint64_t*>(sh.hist + SLICE_BASE + NT);
-  uint64_t* SliceX = reinterpret_cast<uint64_t*>(sh.hist + SLICE_BASE + 3 * NT);
   const int per = max(1, (N + NT - 1) / NT);
-  // exclusive cumulative (p- or q-mass) per entry, when it fits: a search
-  // probe is then one read instead of a walk through its slice
-  const bool cum_ok = N <= CUM_MAX && per <= CUM_PER;
-  uint64_t* CumX = reinterpret_cast<uint64_t*>(sh.hist + ((3 * N + 1) & ~1));
   const int lo = min(N, tid * per), hi = min(N, lo + per);
 
   auto cnt_of = [&](int i) -> uint32_t { return ent[i] & 0xFFFFu; };
-  auto y_raw = [&](int i) -> float { return value_of_order<D>(ent[i] >> 16, CAP, T, sc_entry); };
+  auto y_raw = [&](int i) -> float { return y_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry); };
   const float M = N > 0 ? y_raw(0) : 0.0f;
   if (tid == 0) {
     if (N == 0 || isnan(M)) sh.status |= FL_ROW_NAN;
     else if (isinf(M)) sh.status |= (M > 0.0f) ? FL_ROW_INF : FL_ROW_ALL_MASKED;
   }
   auto Y = [&](int i) -> float { return cached ? Yc[i] : y_raw(i); };
-  auto E = [&](int i) -> float { return cached ? Ec[i] : e_of_order<D>(ent[i] >> 16, CAP, T, sc_entry, M); };
+  auto E = [&](int i) -> float { return cached ? Ec[i] : exp_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry, M); };
   {
     uint32_t lc = 0;
     uint64_t lm = 0;
     for (int i = lo; i < hi; ++i) {
       const uint32_t ord = ent[i] >> 16;
-      const float y = sc_entry ? value_of_order<D>(ord, CAP, T, true)
-                               : temperature_val<D>(D::to_f32(bits_of_order16(ord)), T);
+      const float y = y_of_order<D, SC>(ord, CAP, T, sc_entry);
       const float e = expf(y - M);
       if (cached) {
         Yc[i] = y;
         Ec[i] = e;
+        Cc[i] = lc;  // prefix within the slice; the slice base is added below
+        Cm[i] = lm;
       }
       const uint32_t c = cnt_of(i);
       lc += c;
@@ -407,6 +504,16 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     block_excl_scan2(lc, lm, sh.redu, sh.redq, ec, em, tc, tm);
     SliceCnt[tid] = ec;
     SliceM[tid] = em;
+    if (cached) {
+      for (int i = lo; i < hi; ++i) {
+        Cc[i] += ec;
+        Cm[i] += em;
+      }
+      if (tid == 0) {
+        Cc[N] = tc;
+        Cm[N] = tm;
+      }
+    }
     // a total other than V means a 16-bit counter wrapped (> 65535 equal values)
     if (tid == 0 && tc != static_cast<uint32_t>(V)) atomicOr(&sh.status, FL_ROW_LIMIT);
   }
@@ -414,19 +521,44 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   int32_t status = sh.status;
   FL_MARK(4);
 
-  auto count_before = [&](int L) -> uint32_t {
+  auto count_before = [&](int L) -> uint32_t {  // L in [0, N]
+    if (cached) return Cc[L];
     const int s = min(L / per, NT - 1);
     uint32_t c = SliceCnt[s];
     for (int i = s * per; i < L; ++i) c += cnt_of(i);
     return c;
   };
   auto mass_before = [&](int L) -> uint64_t {
+    if (cached) return Cm[L];
     const int s = min(L / per, NT - 1);
     uint64_t m = SliceM[s];
     for (int i = s * per; i < L; ++i) m += cnt_of(i) * to_fx(E(i));
     return m;
   };
-  const bool w0 = tid < WAVE;  // the wave that runs the searches (results go through sh.dec)
+  const int lane = tid & (WAVE - 1);
+  // Entries of equal value Y form a group (several patterns can round to one
+  // value).  Y is non-increasing along the entries, so a group is a run; the
+  // window of 64 entries next to i settles its bound in one probe unless the
+  // run is longer than that.
+  auto group_lo = [&](int i, float y) -> int {  // first entry j <= i with Y(j) <= y
+    const int w0 = max(0, i - (WAVE - 1));
+    const int j = w0 + lane;
+    const uint64_t m = __ballot(j <= i && Y(j) <= y);
+    if (w0 == 0 || (m & 1ull) == 0) return w0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+    return wave_first(0, w0 + 1, [&](int q) { return Y(q) <= y; });
+  };
+  auto group_hi = [&](int i, float y) -> int {  // last entry j >= i with Y(j) >= y
+    const int j = i + 1 + lane;
+    const uint64_t m = __ballot(j < N && Y(j) < y);
+    if (m) return i + __ffsll(static_cast<unsigned long long>(m)) - 1;
+    if (i + 1 + WAVE >= N) return N - 1;
+    return wave_first(i + 1 + WAVE, N, [&](int q) { return Y(q) < y; }) - 1;
+  };
+  // The serial searches run in wave 0 alone while the other waves wait at a
+  // barrier (running them in every wave would starve the younger waves,
+  // which the SIMDs schedule after the older ones); their results go through
+  // sh.dec.  The scans over many entries use the whole block.
+  const bool w0 = tid < WAVE;
 
   // ---------------- top-k (sampling.py:36-38) and min-p (:40-43): value cuts
   if (status == 0) {
@@ -435,8 +567,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       if (K > 0 && K < V) {
         // first entry whose inclusive count reaches K; every equal value stays
         const int ik = wave_first(0, N, [&](int i) { return count_before(i + 1) >= static_cast<uint32_t>(K); });
-        const float tau = Y(ik);
-        L = wave_first(ik + 1, N, [&](int i) { return Y(i) < tau; });
+        L = group_hi(ik, Y(ik)) + 1;
       }
       double S = from_fx(mass_before(L));
       if (MP > 0.0f) {
@@ -455,120 +586,99 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     __syncthreads();
   }
-  FL_MARK(5);
-  int L = sh.dec.L;
+  const int L = sh.dec.L;
   if (status == 0 && L <= 0) status |= FL_ROW_ALL_MASKED;
-  FL_MARK(11);
+  FL_MARK(5);
 
   // ---------------- top-p (sampling.py:45-51)
   // Position j (descending order) is removed when
   //   round(round_f32(C_j) - p_j) >= round(top_p)
   // with C_j the inclusive cumulative of the rounded probabilities.  The
-  // predicate is monotone along the order, so the kept set is a prefix.
+  // predicate is monotone along the order, so the kept set is a prefix: a
+  // block scan finds the first removed entry (tested on its first member),
+  // then wave 0 counts the kept members of the entry before it.
   if (status == 0) {
     const double S = sh.dec.S;
-    if (TP > 0.0f && TP < 1.0f) {
-      const float r1 = 1.0f / static_cast<float>(S);
-      const float t = D::rn(TP);
-      auto pf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * r1)); };
-      auto removed = [&](uint64_t c_incl, float p) {
-        return D::rn(D::rn(static_cast<float>(from_fx(c_incl))) - p) >= t;
-      };
-      const int lim = min(hi, L);
-      uint64_t local = 0;
-      {
-        for (int i = lo; i < lim; ++i) local += cnt_of(i) * pf(i);
-      }
-      uint64_t tot;
-      const uint64_t sb = block_excl_scan<uint64_t>(local, sh.redq, &tot);
-      SliceX[tid] = sb;
-      if (cum_ok) {
-        uint64_t c = sb;
-        for (int i = lo; i < lim; ++i) {
-          CumX[i] = c;
-          c += cnt_of(i) * pf(i);
-        }
-      }
-      __syncthreads();
-      if (w0) {
-        auto cx = [&](int i) -> uint64_t {  // p-mass before entry i (exact fixed point)
-          if (cum_ok) return CumX[i];
-          const int s = i / per;
-          uint64_t c = SliceX[s];
-          for (int j = s * per; j < i; ++j) c += cnt_of(j) * pf(j);
-          return c;
-        };
-        const int i1 = wave_first(0, L, [&](int i) { return removed(cx(i) + pf(i), D::rn(E(i) * r1)); });
-        int i0 = L - 1;
-        uint32_t c0 = cnt_of(L - 1);
-        if (i1 == 0) {
-          i0 = -1;
-        } else if (i1 < L) {
-          i0 = i1 - 1;
-          const uint64_t c = cx(i0);
-          const float p = D::rn(E(i0) * r1);
-          const uint64_t pfi = to_fx(p);
-          // member j of entry i0 is removed iff removed(c + (j+1) pf, p);
-          // member 0 is known to survive
-          c0 = static_cast<uint32_t>(wave_first(1, static_cast<int>(cnt_of(i0)), [&](int j) {
-            return removed(c + static_cast<uint64_t>(j + 1) * pfi, p);
-          }));
-        }
-        if (tid == 0) {
-          sh.dec.i0 = i0;
-          sh.dec.c0 = c0;
-        }
-      }
-    } else if (tid == 0) {
-      sh.dec.i0 = L - 1;
-      sh.dec.c0 = cnt_of(L - 1);
-    }
-    __syncthreads();
-  }
-  FL_MARK(15);
-
-  // ---------------- cut group, softmax (:58) and selection (:59-61)
-  int i0 = sh.dec.i0;
-  uint32_t c0 = sh.dec.c0;
-  if (status == 0 && i0 < 0) status |= FL_ROW_ALL_MASKED;
-  if (status == 0) {
+    int i0 = L - 1;
+    uint32_t c0 = cnt_of(L - 1);
+    const float r1 = 1.0f / static_cast<float>(S);
+    const float t = D::rn(TP);
+    auto pf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * r1)); };
+    auto removed = [&](uint64_t c_incl, float p) {
+      return D::rn(D::rn(static_cast<float>(from_fx(c_incl))) - p) >= t;
+    };
+    ScanHit h = {L, 0ull, 0ull};
+    if (TP > 0.0f && TP < 1.0f)
+      h = scan_first(sh, L, false, 0ull, [&](int i) { return cnt_of(i) * pf(i); },
+                     [&](int i, uint64_t ex, uint64_t) { return removed(ex + pf(i), D::rn(E(i) * r1)); });
+    FL_MARK(15);
     if (w0) {
-      const float ycut = Y(i0);
-      const int cut_lo = wave_first(0, i0 + 1, [&](int i) { return Y(i) <= ycut; });
-      const int cut_hi = wave_first(i0 + 1, N, [&](int i) { return Y(i) < ycut; }) - 1;
-      const uint32_t n_before_i0 = count_before(i0);
-      const uint32_t n_before_lo = count_before(cut_lo);
-      const double SK = from_fx(mass_before(i0) + c0 * to_fx(E(i0)));
+      if (h.idx == 0) {
+        i0 = -1;
+      } else if (h.idx < L) {
+        i0 = h.idx - 1;
+        const float p = D::rn(E(i0) * r1);
+        const uint64_t pfi = to_fx(p);
+        const uint64_t c = h.excl - cnt_of(i0) * pfi;  // p-mass before entry i0
+        // member j of entry i0 is removed iff removed(c + (j+1) pf, p); member
+        // 0 survives (entry i0 is not removed)
+        c0 = static_cast<uint32_t>(wave_first(1, static_cast<int>(cnt_of(i0)), [&](int j) {
+          return removed(c + static_cast<uint64_t>(j + 1) * pfi, p);
+        }));
+      }
+      // the group of the cut value, the kept count and the kept mass (:58)
+      if (i0 >= 0) {
+        const float ycut = Y(i0);
+        const int cut_lo = group_lo(i0, ycut);
+        const int cut_hi = group_hi(i0, ycut);
+        const uint32_t n_before_i0 = count_before(i0);
+        const uint32_t n_before_lo = count_before(cut_lo);
+        const double SK = from_fx(mass_before(i0) + c0 * to_fx(E(i0)));
+        const uint32_t cut_total = count_before(cut_hi + 1) - n_before_lo;
+        if (tid == 0) {
+          sh.dec.cut_total = cut_total;
+          sh.dec.cut_kept = n_before_i0 - n_before_lo + c0;
+          sh.dec.cut_lo = cut_lo;
+          sh.dec.cut_hi = cut_hi;
+          sh.dec.n_kept = n_before_i0 + c0;
+          sh.dec.SK = SK;
+          sh.dec.y_cut = ycut;
+          sh.dec.o_lo[1] = ent[cut_lo] >> 16;
+          sh.dec.o_hi[1] = ent[cut_hi] >> 16;
+        }
+      }
       if (tid == 0) {
-        sh.dec.cut_total = count_before(cut_hi + 1) - n_before_lo;
-        sh.dec.cut_kept = n_before_i0 - n_before_lo + c0;
-        sh.dec.cut_lo = cut_lo;
-        sh.dec.cut_hi = cut_hi;
-        sh.dec.n_kept = n_before_i0 + c0;
-        sh.dec.SK = SK;
-        sh.dec.y_cut = ycut;
+        sh.dec.i0 = i0;
+        sh.dec.c0 = c0;
       }
     }
     __syncthreads();
   }
+  const int i0 = sh.dec.i0;
+  const uint32_t c0 = sh.dec.c0;
+  if (status == 0 && i0 < 0) status |= FL_ROW_ALL_MASKED;
   const double SK = sh.dec.SK;
   const float rK = 1.0f / static_cast<float>(SK);
   const uint32_t n_kept = sh.dec.n_kept;
+  const uint32_t cut_kept = sh.dec.cut_kept, cut_total = sh.dec.cut_total;
+  const float y_cut = status == 0 ? sh.dec.y_cut : __builtin_inff();
+
+  // ---------------- selection (:59-61)
   auto kc = [&](int i) -> uint32_t { return i < i0 ? cnt_of(i) : (i == i0 ? c0 : 0u); };
   auto kept_before = [&](int Lb) -> uint32_t { return Lb <= i0 ? count_before(Lb) : n_kept; };
-  if (status == 0 && select) {
+  const bool want_sel = select && status == 0;
+  if (want_sel) {
     if (T <= 0.0f) {
       // greedy (sampling.py:59-60): first index among the maximal probabilities
       if (w0) {
         const float qmax = D::rn(E(0) * rK);
         const int last = wave_first(1, i0 + 1, [&](int i) { return D::rn(E(i) * rK) != qmax; }) - 1;
-        const float yl = Y(last);
-        const int sh_hi = wave_first(last + 1, N, [&](int i) { return Y(i) < yl; }) - 1;
+        const int sh_hi = group_hi(last, Y(last));
         if (tid == 0) {
-          sh.dec.sel_lo = 0;
-          sh.dec.sel_hi = sh_hi;
           sh.dec.sel_rank = 0;
           sh.dec.y_sel = Y(0);
+          sh.dec.o_lo[0] = ent[0] >> 16;
+          sh.dec.o_hi[0] = ent[sh_hi] >> 16;
         }
       }
     } else {
@@ -576,125 +686,116 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       // first member whose inclusive cumulative probability exceeds u * total,
       // cumulative sums in exact 2^-46 fixed point
       auto qf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * rK)); };
-      const int lim = min(hi, i0 + 1);
-      uint64_t local = 0;
-      {
-        for (int i = lo; i < lim; ++i) local += kc(i) * qf(i);
+      const int n = i0 + 1;
+      uint64_t Q = 0;
+      if (n > NT) {  // several scan rounds: the total first
+        uint64_t local = 0;
+        for (int i = tid; i < n; i += NT) local += kc(i) * qf(i);
+        Q = block_reduce(local, OpAdd(), sh.redq);
       }
-      uint64_t Q;
-      const uint64_t sb = block_excl_scan<uint64_t>(local, sh.redq, &Q);
-      SliceX[tid] = sb;
-      if (cum_ok) {
-        uint64_t c = sb;
-        for (int i = lo; i < lim; ++i) {
-          CumX[i] = c;
-          c += kc(i) * qf(i);
-        }
-      }
-      __syncthreads();
+      auto target_of = [&](uint64_t q) { return __double2ull_rd(static_cast<double>(U) * static_cast<double>(q)); };
+      const ScanHit h = scan_first(sh, n, n > NT, Q, [&](int i) { return kc(i) * qf(i); },
+                                   [&](int i, uint64_t ex, uint64_t tq) { return ex + kc(i) * qf(i) > target_of(tq); });
       if (w0) {
-        auto cq = [&](int i) -> uint64_t {  // q-mass before entry i
-          if (cum_ok) return CumX[i];
-          const int s = i / per;
-          uint64_t c = SliceX[s];
-          for (int j = s * per; j < i; ++j) c += kc(j) * qf(j);
-          return c;
-        };
-        const uint64_t target = __double2ull_rd(static_cast<double>(U) * static_cast<double>(Q));
-        int is = wave_first(0, i0 + 1, [&](int i) { return cq(i) + kc(i) * qf(i) > target; });
-        if (is > i0) is = 0;  // no positive mass at all (every kept probability rounds to zero)
+        const uint64_t target = target_of(h.total);
+        int is = h.idx;
+        uint64_t ex = h.excl;
+        if (is > i0) {  // no positive mass at all (every kept probability rounds to zero)
+          is = 0;
+          ex = 0;
+        }
         const float ys = Y(is);
-        const int s_lo = wave_first(0, is + 1, [&](int i) { return Y(i) <= ys; });
-        const int s_hi = wave_first(is + 1, N, [&](int i) { return Y(i) < ys; }) - 1;
-        const uint64_t cg = cq(s_lo);
+        const int s_lo = group_lo(is, ys), s_hi = group_hi(is, ys);
+        // q-mass before the group: the scan's prefix at `is` less the group's
+        // entries before it
+        uint64_t inner = 0;
+        for (int j = s_lo + lane; j < is; j += WAVE) inner += kc(j) * qf(j);
+        const uint64_t cg = ex - wave_reduce(inner, OpAdd());
         const uint64_t q = qf(is);
         const uint32_t kept_g = kept_before(s_hi + 1) - kept_before(s_lo);
         // member r of the group covers [cg + r q, cg + (r+1) q)
         const uint64_t r = (q > 0 && target >= cg) ? (target - cg) / q : 0;
         if (tid == 0) {
-          sh.dec.sel_lo = s_lo;
-          sh.dec.sel_hi = s_hi;
           sh.dec.sel_rank = static_cast<uint32_t>(min(r, static_cast<uint64_t>(kept_g > 0 ? kept_g - 1 : 0)));
           sh.dec.y_sel = ys;
+          sh.dec.o_lo[0] = ent[s_lo] >> 16;
+          sh.dec.o_hi[0] = ent[s_hi] >> 16;
         }
       }
     }
-    __syncthreads();
   }
-  const int cut_lo = sh.dec.cut_lo, cut_hi = sh.dec.cut_hi;
-  const uint32_t cut_kept = sh.dec.cut_kept, cut_total = sh.dec.cut_total;
-  const int sel_lo = sh.dec.sel_lo, sel_hi = sh.dec.sel_hi;
-  const uint32_t sel_rank = sh.dec.sel_rank;
-  const float y_sel = sh.dec.y_sel;
-  const float y_cut = status == 0 ? sh.dec.y_cut : __builtin_inff();
   FL_MARK(6);
 
   // ------------------------------------------------ identification
   // Targets: 0 = selected token (group sel, rank sel_rank); 1 = last kept
   // member of a partially kept group (for the descriptor's idx_cut).
   const bool want_cut = (a.out_desc != nullptr) && status == 0 && cut_kept < cut_total;
-  const bool want_sel = select && status == 0;
-  uint32_t o_lo[2] = {0, 0}, o_hi[2] = {0, 0}, rank[2] = {0, 0};
-  bool active[2] = {want_sel, want_cut};
-  if (want_sel) { o_lo[0] = ent[sel_lo] >> 16; o_hi[0] = ent[sel_hi] >> 16; rank[0] = sel_rank; }
-  if (want_cut) { o_lo[1] = ent[cut_lo] >> 16; o_hi[1] = ent[cut_hi] >> 16; rank[1] = cut_kept - 1; }
-  __syncthreads();  // entries are overwritten by the candidate lists below
-
-  if (active[0] || active[1]) {
+  float y_sel = 0.0f;
+  if (want_sel || want_cut) {
+    // The row tile: the first read, still in VGPRs, or (soft-cap kernel,
+    // whose calls keep it from staying there) the row read again.  A re-read
+    // is issued here, not during the decisions: a wave stalls issuing loads
+    // while the memory system is backed up, which would stall the search wave.
+    uint4 r[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if constexpr (SC) r[j] = fast ? buf_load16(rrow, 16u * tid, 16u * NT * j) : make_uint4(0, 0, 0, 0);
+      else r[j] = d[j];
+    }
+    lds_barrier();  // the decisions are in sh.dec; the entries may be overwritten
+    FL_MARK(13);
+    y_sel = sh.dec.y_sel;
+    const uint32_t o_lo[2] = {sh.dec.o_lo[0], sh.dec.o_lo[1]};
+    const uint32_t o_hi[2] = {sh.dec.o_hi[0], sh.dec.o_hi[1]};
+    const uint32_t rank[2] = {sh.dec.sel_rank, cut_kept - 1};
+    const bool active[2] = {want_sel, want_cut};
     uint32_t* list[2] = {sh.hist, sh.hist + LIST_CAP};
-    uint32_t* hitq = sh.hist + 2 * LIST_CAP;
     auto in_range = [&](int t, uint32_t bits) { return order16(bits) - o_lo[t] <= o_hi[t] - o_lo[t]; };
     auto is_hist = [&](int idx) { return pen && ((sh.hbits[idx >> 5] >> (idx & 31)) & 1u); };
-    // The targets' order ranges as at most four ranges of raw bit patterns
-    // (a range across zero splits into its positive and negative parts).
-    // (slots 2t, 2t+1 belong to target t; fixed slots keep the arrays in VGPRs)
-    // Range r covers patterns rlo[r] .. rlo[r] + rw[r].
-    uint32_t rlo[4] = {0, 0, 0, 0}, rw[4] = {0, 0, 0, 0};
-    bool ren[4] = {false, false, false, false};
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (!active[t]) continue;
-      if (o_hi[t] < 0x8000u) {
-        rlo[2 * t] = 0x7FFFu - o_hi[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
-      } else if (o_lo[t] >= 0x8000u) {
-        rlo[2 * t] = o_lo[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
-      } else {
-        rlo[2 * t] = 0u, rw[2 * t] = 0x7FFFu - o_lo[t], ren[2 * t] = true;
-        rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
-      }
-    }
-    auto candidate = [&](int idx, int t) {
-      if (idx < V && !is_hist(idx)) {
-        const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
-        if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = idx;
-      }
+    auto push = [&](int t, int idx) {
+      const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
+      if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = idx;
     };
-    // Element work for one chunk (patterns recomputed one by one).
+    // Element work for one chunk: non-history elements whose pattern lies in
+    // a target group.
     auto chunk_candidates = [&](int c, const uint4 q) {
       const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t bits = elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
+        const int idx = c * 8 + e;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          if (active[t] && in_range(t, bits)) candidate(c * 8 + e, t);
+          if (active[t] && in_range(t, bits) && idx < V && !is_hist(idx)) push(t, idx);
       }
     };
     const int nchunks = (V + 7) >> 3;
     if (fast) {
-      // Non-history elements whose value lies in a target group.  The row is
-      // read again (mostly a cache hit: keeping the VGPR tile through the
-      // decisions would spill), each chunk gets a branch-free packed test, and
-      // the rare hit chunks are queued in LDS with their data, to be examined
-      // element by element by all threads afterwards.
-      uint4 r[NCH];
+      // The targets' order ranges as at most four ranges of raw bit patterns
+      // (a range across zero splits into its positive and negative parts).
+      // (slots 2t, 2t+1 belong to target t; fixed slots keep the arrays in
+      // VGPRs.)  Range r covers patterns rlo[r] .. rlo[r] + rw[r].
+      uint32_t rlo[4] = {0, 0, 0, 0}, rw[4] = {0, 0, 0, 0};
+      bool ren[4] = {false, false, false, false};
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) r[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
-      FL_MARK(13);
+      for (int t = 0; t < 2; ++t) {
+        if (!active[t]) continue;
+        if (o_hi[t] < 0x8000u) {
+          rlo[2 * t] = 0x7FFFu - o_hi[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+        } else if (o_lo[t] >= 0x8000u) {
+          rlo[2 * t] = o_lo[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+        } else {
+          rlo[2 * t] = 0u, rw[2 * t] = 0x7FFFu - o_lo[t], ren[2 * t] = true;
+          rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
+        }
+      }
+      // a branch-free packed test per chunk: (w - lo) per 16-bit half, the
+      // minimum over the chunk's 8 elements is <= width iff the chunk holds a
+      // member of the range.  The rare hit chunks then get per-element member
+      // masks, bit 8 (j % 4) + e of mask word j / 4 for element e of chunk j.
+      uint32_t mk[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        // packed (w - lo) per half, minimum over the chunk's 8 elements: a
-        // chunk holds a member of range rr iff that minimum is <= width
         bool hit = false;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -706,52 +807,42 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
               __builtin_elementwise_min(__builtin_bit_cast(u16x2, r[j].z) - lo2, __builtin_bit_cast(u16x2, r[j].w) - lo2));
           hit |= min(static_cast<uint32_t>(m[0]), static_cast<uint32_t>(m[1])) <= rw[rr];
         }
-        const int c = j * NT + tid;
-        if (hit && c < nchunks) {
-          const uint32_t s = atomicAdd(&sh.nhit, 1u);
-          if (s < static_cast<uint32_t>(HIT_CAP)) {
-            hitq[5 * s] = c;
-            hitq[5 * s + 1] = r[j].x;
-            hitq[5 * s + 2] = r[j].y;
-            hitq[5 * s + 3] = r[j].z;
-            hitq[5 * s + 4] = r[j].w;
+        if (hit && j * NT + tid < nchunks) {
+          const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t bits = (w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              mk[t][j >> 2] |= (active[t] && in_range(t, bits)) ? (1u << (8 * (j & 3) + e)) : 0u;
           }
         }
       }
       FL_MARK(14);
-      __syncthreads();
-    }
-    {
-      // the queued chunks, or every chunk when the queue overflowed or the
-      // row is not in the VGPR tile
-      const uint32_t nhit = sh.nhit;
-      const bool use_queue = fast && nhit <= static_cast<uint32_t>(HIT_CAP);
-      const int n_iter = use_queue ? static_cast<int>(nhit) : nchunks;
-      for (int i = tid; i < n_iter; i += NT) {
-        int c = i;
-        uint4 q;
-        if (use_queue) {
-          c = static_cast<int>(hitq[5 * i]);
-          q = make_uint4(hitq[5 * i + 1], hitq[5 * i + 2], hitq[5 * i + 3], hitq[5 * i + 4]);
-        } else {
-          q = fast ? buf_load16(rrow, 16u * c, 0u) : load_chunk16(row, c, V, ALIGNED);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t m = mk[t][q];
+          while (m) {
+            const int bit = __ffs(m) - 1;
+            m &= m - 1u;
+            const int idx = ((4 * q + (bit >> 3)) * NT + tid) * 8 + (bit & 7);
+            if (idx < V && !is_hist(idx)) push(t, idx);
+          }
         }
-        chunk_candidates(c, q);
       }
+    } else {
+      for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, load_chunk16(row, c, V, ALIGNED));
     }
     // history elements whose penalised value lies in a target group (the
     // first HPRE ids of each thread and their logits are still in registers)
     if (pen) {
       auto hist_candidate = [&](int id, uint32_t raw) {
-        const uint32_t z = elem_bits(raw);
-        const uint32_t zp = penalised_bits<D>(z, RP);
+        const uint32_t zp = penalised_bits<D>(elem_bits(raw), RP);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          if (active[t] && in_range(t, zp)) {
-            const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
-            if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = id;
-          }
-        }
+        for (int t = 0; t < 2; ++t)
+          if (active[t] && in_range(t, zp)) push(t, id);
       };
 #pragma unroll
       for (int k = 0; k < HPRE; ++k)
@@ -764,15 +855,28 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     __syncthreads();
     FL_MARK(7);
-    // The member of rank r (by index) among a target's candidates: bucket
-    // counts over 128-index buckets locate the bucket holding rank r, and a
-    // 128-bit mask of that bucket's members gives the index.
-    uint32_t* bins = sh.hist + 2 * LIST_CAP;  // the hit queue is no longer needed
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
       const int n = static_cast<int>(sh.nlist[t]);
-      if (n <= LIST_CAP) {
+      if (n <= WAVE) {
+        // few candidates: wave 0 ranks them (indices are distinct) by counting
+        if (tid < WAVE) {
+          const uint32_t v = lane < n ? list[t][lane] : 0xFFFFFFFFu;
+          uint32_t below = 0;
+          for (int k = 0; k < n; ++k)
+            below += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), k)) < v ? 1u : 0u;
+          const uint64_t m = __ballot(lane < n && below == rank[t]);
+          if (m) {
+            const int res = __builtin_amdgcn_readlane(static_cast<int>(v), __ffsll(static_cast<unsigned long long>(m)) - 1);
+            if (tid == 0) sh.result[t] = res;
+          }
+        }
+      } else if (n <= LIST_CAP) {
+        // The member of rank r (by index): bucket counts over 128-index
+        // buckets locate the bucket holding rank r, and a 128-bit mask of
+        // that bucket's members gives the index.
+        uint32_t* bins = sh.hist + 2 * LIST_CAP;
         for (int i = tid; i < RANK_BINS + 4; i += NT) bins[i] = 0;
         if (tid == 0) sh.rank_bin = 0xFFFFFFFFu;
         __syncthreads();
@@ -820,6 +924,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
             need -= pc;
           }
         }
+        __syncthreads();
       } else {
         // the candidate list overflowed: count matches round by round in
         // index order (re-reads the row from memory; a rare path)
@@ -848,11 +953,10 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
           base += tot;
           if (base > rank[t]) break;
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
-  __syncthreads();
   FL_MARK(8);
 
   // ------------------------------------------------ outputs
@@ -902,8 +1006,14 @@ hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s) {
   const bool has_pen = a.rep_penalty != nullptr && a.hist_ids != nullptr && a.hist_len != nullptr;
   const int sc_elem = (a.softcap > 0.0f && has_pen) ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(a.batch)), block(NT);
-  if (a.dtype == FL_DTYPE_BF16) hipLaunchKernelGGL(k_sample_rows16<BF16>, grid, block, 0, s, a, aligned, sc_elem);
-  else hipLaunchKernelGGL(k_sample_rows16<F16>, grid, block, 0, s, a, aligned, sc_elem);
+  const bool sc = a.softcap > 0.0f;
+  if (a.dtype == FL_DTYPE_BF16) {
+    if (sc) hipLaunchKernelGGL((k_sample_rows16<BF16, true>), grid, block, 0, s, a, aligned, sc_elem);
+    else hipLaunchKernelGGL((k_sample_rows16<BF16, false>), grid, block, 0, s, a, aligned, sc_elem);
+  } else {
+    if (sc) hipLaunchKernelGGL((k_sample_rows16<F16, true>), grid, block, 0, s, a, aligned, sc_elem);
+    else hipLaunchKernelGGL((k_sample_rows16<F16, false>), grid, block, 0, s, a, aligned, sc_elem);
+  }
   return hipGetLastError();
 }
 
