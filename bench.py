@@ -171,7 +171,7 @@ def main() -> int:
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
                      "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
                      "kernel_ms_p10": durs[len(durs) // 10], "kernel_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": "k_sample_rows16<BF16>" if w.logits.element_size() == 2 else "k_sample_rows32"},
+                     "kernel": "k_sample_rows16<BF16, false>" if w.logits.element_size() == 2 else "k_sample_rows32"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
