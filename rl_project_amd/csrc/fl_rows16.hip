@@ -31,8 +31,7 @@ constexpr int NCH = 16;                          // 16-byte chunks per thread
 constexpr int HIST_WORDS = 32768;                // 65536 packed u16 counters
 constexpr int HBITS_WORDS = FL_MAX_VOCAB_16 / 32;
 constexpr int OWNER_WORDS = FL_MAX_HISTORY / 32;
-constexpr int LIST_CAP = HIST_WORDS / 4;          // candidates per identification target
-constexpr int RANK_BINS = FL_MAX_VOCAB_16 / 128;  // index buckets of the rank selection
+constexpr int HLIST_CAP = HIST_WORDS / 8;         // history members listed per identification target
 constexpr int SLICE_BASE = HIST_WORDS - 3 * NT;   // slice tables: count u32[NT], mass u64[NT]
 constexpr int ENT_MAX = SLICE_BASE;               // entries (distinct values) a row may have
 constexpr int CACHE_MAX = (SLICE_BASE - 4) / 6;   // entries with y, e, prefix count and mass kept per entry
@@ -61,8 +60,8 @@ struct Shared16 {
     uint32_t o_lo[2], o_hi[2];
     float y_sel, y_cut;
   } dec;  // results of the search wave
-  uint32_t nlist[2];
-  uint32_t rank_bin, rank_in_bin;
+  uint32_t slot[2][NCH];  // identification: members per slot of NT chunks
+  uint32_t nh[2];         // identification: history members
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -238,9 +237,10 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(sh.hist)[tid + k * NT] = make_uint4(0, 0, 0, 0);
   reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
   if (tid < OWNER_WORDS / 4) reinterpret_cast<uint4*>(sh.owner)[tid] = make_uint4(0, 0, 0, 0);
+  if (tid < 2 * NCH) (&sh.slot[0][0])[tid] = 0;
   if (tid == 0) {
     sh.status = 0;
-    sh.nlist[0] = sh.nlist[1] = 0;
+    sh.nh[0] = sh.nh[1] = 0;
     sh.result[0] = sh.result[1] = -1;
     sh.dec.L = 0;
     sh.dec.i0 = -1;
@@ -607,19 +607,22 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     auto removed = [&](uint64_t c_incl, float p) {
       return D::rn(D::rn(static_cast<float>(from_fx(c_incl))) - p) >= t;
     };
+    const bool top_p = TP > 0.0f && TP < 1.0f;
     ScanHit h = {L, 0ull, 0ull};
-    if (TP > 0.0f && TP < 1.0f)
+    if (top_p)
       h = scan_first(sh, L, false, 0ull, [&](int i) { return cnt_of(i) * pf(i); },
                      [&](int i, uint64_t ex, uint64_t) { return removed(ex + pf(i), D::rn(E(i) * r1)); });
     FL_MARK(15);
     if (w0) {
-      if (h.idx == 0) {
+      if (top_p && h.idx == 0) {
         i0 = -1;
-      } else if (h.idx < L) {
+      } else if (top_p) {
+        // the entry before the first removed one (the last entry when none
+        // is removed) may lose its later members
         i0 = h.idx - 1;
         const float p = D::rn(E(i0) * r1);
         const uint64_t pfi = to_fx(p);
-        const uint64_t c = h.excl - cnt_of(i0) * pfi;  // p-mass before entry i0
+        const uint64_t c = h.excl - cnt_of(i0) * pfi;  // p-mass before entry i0 (h.excl: before entry idx)
         // member j of entry i0 is removed iff removed(c + (j+1) pf, p); member
         // 0 survives (entry i0 is not removed)
         c0 = static_cast<uint32_t>(wave_first(1, static_cast<int>(cnt_of(i0)), [&](int j) {
@@ -742,111 +745,135 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       if constexpr (SC) r[j] = fast ? buf_load16(rrow, 16u * tid, 16u * NT * j) : make_uint4(0, 0, 0, 0);
       else r[j] = d[j];
     }
+    // the logits of this thread's first HPRE history ids again (keeping them
+    // in VGPRs since the count pass would spill them), issued now so that the
+    // loads overlap the member counting
+    // (a buffer load by 32-bit offset: nothing 64-bit to keep from the first
+    // read of these logits)
+    const __amdgpu_buffer_rsrc_t rall = row_rsrc(row, 2u * static_cast<uint32_t>(V));
+    uint32_t xh2[HPRE];
+#pragma unroll
+    for (int k = 0; k < HPRE; ++k)
+      xh2[k] = __builtin_amdgcn_raw_buffer_load_b16(rall, own[k] ? 2 * hpre[k] : 0, 0, 0);
     lds_barrier();  // the decisions are in sh.dec; the entries may be overwritten
     FL_MARK(13);
     y_sel = sh.dec.y_sel;
-    const uint32_t o_lo[2] = {sh.dec.o_lo[0], sh.dec.o_lo[1]};
-    const uint32_t o_hi[2] = {sh.dec.o_hi[0], sh.dec.o_hi[1]};
-    const uint32_t rank[2] = {sh.dec.sel_rank, cut_kept - 1};
+    // (wave-uniform values: kept in SGPRs, the VGPRs hold the tile)
+    auto uni = [](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v))); };
+    const uint32_t o_lo[2] = {uni(sh.dec.o_lo[0]), uni(sh.dec.o_lo[1])};
+    const uint32_t o_hi[2] = {uni(sh.dec.o_hi[0]), uni(sh.dec.o_hi[1])};
+    const uint32_t rank[2] = {uni(sh.dec.sel_rank), uni(cut_kept - 1)};
     const bool active[2] = {want_sel, want_cut};
-    uint32_t* list[2] = {sh.hist, sh.hist + LIST_CAP};
+    // Members of a target, in the order of the convention (ascending
+    // vocabulary index), which is also the order of the tile: element e of
+    // chunk j * NT + tid has index (j * NT + tid) * 8 + e, so indices go by
+    // (j, tid, e).  History ids are members by their penalised value (their
+    // owners test them and list them); other elements by their pattern.
+    // Every chunk's members are counted (branch-free, packed), giving the
+    // members of each slot j (chunks j * NT .. j * NT + NT - 1); only in the
+    // slot of rank r do the threads form their members, and a block scan
+    // picks the one of rank r.
+    uint32_t* hlist[2] = {sh.hist, sh.hist + HLIST_CAP};
     auto in_range = [&](int t, uint32_t bits) { return order16(bits) - o_lo[t] <= o_hi[t] - o_lo[t]; };
     auto is_hist = [&](int idx) { return pen && ((sh.hbits[idx >> 5] >> (idx & 31)) & 1u); };
     auto push = [&](int t, int idx) {
-      const uint32_t s = atomicAdd(&sh.nlist[t], 1u);
-      if (s < static_cast<uint32_t>(LIST_CAP)) list[t][s] = idx;
+      const uint32_t s = atomicAdd(&sh.nh[t], 1u);
+      if (s < static_cast<uint32_t>(HLIST_CAP)) hlist[t][s] = idx;
     };
-    // Element work for one chunk: non-history elements whose pattern lies in
-    // a target group.
-    auto chunk_candidates = [&](int c, const uint4 q) {
+    // non-history members of chunk c (8 patterns in q): bit e for element e
+    auto chunk_mask = [&](int t, int c, const uint4 q) -> uint32_t {
       const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+      uint32_t m = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t bits = elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
-        const int idx = c * 8 + e;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          if (active[t] && in_range(t, bits) && idx < V && !is_hist(idx)) push(t, idx);
-      }
+      for (int e = 0; e < 8; ++e) m |= in_range(t, elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu)) ? (1u << e) : 0u;
+      const int nv = V - c * 8;
+      uint32_t valid = nv >= 8 ? 0xFFu : (nv > 0 ? (1u << nv) - 1u : 0u);
+      if (pen) valid &= ~(sh.hbits[c >> 2] >> ((c & 3) * 8));
+      return m & valid;
     };
     const int nchunks = (V + 7) >> 3;
-    if (fast) {
-      // The targets' order ranges as at most four ranges of raw bit patterns
-      // (a range across zero splits into its positive and negative parts).
-      // (slots 2t, 2t+1 belong to target t; fixed slots keep the arrays in
-      // VGPRs.)  Range r covers patterns rlo[r] .. rlo[r] + rw[r].
-      uint32_t rlo[4] = {0, 0, 0, 0}, rw[4] = {0, 0, 0, 0};
-      bool ren[4] = {false, false, false, false};
+    // Raw patterns of the targets as at most four ranges (a range across zero
+    // splits into its positive and negative parts); slots 2t, 2t+1 belong to
+    // target t (fixed slots keep the arrays in registers).  Range r covers
+    // patterns rlo[r] .. rlo[r] + rw[r].
+    uint32_t rlo[4] = {0, 0, 0, 0}, rw[4] = {0, 0, 0, 0};
+    bool ren[4] = {false, false, false, false};
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (!active[t]) continue;
-        if (o_hi[t] < 0x8000u) {
-          rlo[2 * t] = 0x7FFFu - o_hi[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
-        } else if (o_lo[t] >= 0x8000u) {
-          rlo[2 * t] = o_lo[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
-        } else {
-          rlo[2 * t] = 0u, rw[2 * t] = 0x7FFFu - o_lo[t], ren[2 * t] = true;
-          rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
-        }
+    for (int t = 0; t < 2; ++t) {
+      if (!active[t]) continue;
+      if (o_hi[t] < 0x8000u) {
+        rlo[2 * t] = 0x7FFFu - o_hi[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+      } else if (o_lo[t] >= 0x8000u) {
+        rlo[2 * t] = o_lo[t], rw[2 * t] = o_hi[t] - o_lo[t], ren[2 * t] = true;
+      } else {
+        rlo[2 * t] = 0u, rw[2 * t] = 0x7FFFu - o_lo[t], ren[2 * t] = true;
+        rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
       }
-      // a branch-free packed test per chunk: (w - lo) per 16-bit half, the
-      // minimum over the chunk's 8 elements is <= width iff the chunk holds a
-      // member of the range.  The rare hit chunks then get per-element member
-      // masks, bit 8 (j % 4) + e of mask word j / 4 for element e of chunk j.
-      uint32_t mk[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        bool hit = false;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          if (!ren[rr]) continue;  // wave-uniform
-          const unsigned short l16 = static_cast<unsigned short>(rlo[rr]);
-          const u16x2 lo2 = {l16, l16};
-          const u16x2 m = __builtin_elementwise_min(
-              __builtin_elementwise_min(__builtin_bit_cast(u16x2, r[j].x) - lo2, __builtin_bit_cast(u16x2, r[j].y) - lo2),
-              __builtin_elementwise_min(__builtin_bit_cast(u16x2, r[j].z) - lo2, __builtin_bit_cast(u16x2, r[j].w) - lo2));
-          hit |= min(static_cast<uint32_t>(m[0]), static_cast<uint32_t>(m[1])) <= rw[rr];
-        }
-        if (hit && j * NT + tid < nchunks) {
-          const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t bits = (w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-              mk[t][j >> 2] |= (active[t] && in_range(t, bits)) ? (1u << (8 * (j & 3) + e)) : 0u;
-          }
-        }
-      }
-      FL_MARK(14);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t m = mk[t][q];
-          while (m) {
-            const int bit = __ffs(m) - 1;
-            m &= m - 1u;
-            const int idx = ((4 * q + (bit >> 3)) * NT + tid) * 8 + (bit & 7);
-            if (idx < V && !is_hist(idx)) push(t, idx);
-          }
-        }
-      }
-    } else {
-      for (int c = tid; c < nchunks; c += NT) chunk_candidates(c, load_chunk16(row, c, V, ALIGNED));
     }
-    // history elements whose penalised value lies in a target group (the
-    // first HPRE ids of each thread and their logits are still in registers)
+    // Per chunk, branch-free, the members of each range: for a half
+    // d = w - lo, min(d, 0x8000) - (width + 1) has its top bit set iff
+    // d <= width (width + 1 <= 0x8000); the shifted-down top bits summed
+    // over the chunk's words count its members.  (Written as instructions:
+    // the compiler would turn the arithmetic back into compares.)
+    const uint32_t c8000 = 0x80008000u, c15 = 0x000F000Fu;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (!active[t]) continue;
+      if (fast) {
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          uint32_t acc = 0;
+#pragma unroll
+          for (int rr = 2 * t; rr < 2 * t + 2; ++rr) {
+            if (!ren[rr]) continue;  // wave-uniform
+            const uint32_t lo2 = rlo[rr] * 0x10001u, th2 = (rw[rr] + 1u) * 0x10001u;
+            const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              uint32_t f;
+              asm("v_pk_sub_u16 %0, %1, %2\n\t"
+                  "v_pk_min_u16 %0, %0, %3\n\t"
+                  "v_pk_sub_u16 %0, %0, %4\n\t"
+                  "v_pk_lshrrev_b16 %0, %5, %0"
+                  : "=&v"(f)
+                  : "v"(w4[k]), "s"(lo2), "s"(c8000), "s"(th2), "s"(c15));
+              acc += f;  // halves count separately: at most 16 per half
+            }
+          }
+          uint32_t cj = (acc & 0xFFFFu) + (acc >> 16);
+          const int c = j * NT + tid;
+          if (c >= nchunks) cj = 0;
+          else if (c == nfull && in_range(t, 0u)) cj -= static_cast<uint32_t>(8 - (V - c * 8));  // zero padding
+          if (cj) atomicAdd(&sh.slot[t][j], cj);
+        }
+      } else {
+        for (int j = 0; j < NCH; ++j) {
+          const int c = j * NT + tid;
+          if (c >= nchunks) break;
+          const uint32_t cj = static_cast<uint32_t>(__popc(chunk_mask(t, c, load_chunk16(row, c, V, ALIGNED))));
+          if (cj) atomicAdd(&sh.slot[t][j], cj);
+        }
+      }
+    }
+    FL_MARK(14);
+    // history elements whose penalised value lies in a target group
     if (pen) {
       auto hist_candidate = [&](int id, uint32_t raw) {
-        const uint32_t zp = penalised_bits<D>(elem_bits(raw), RP);
+        const uint32_t z = elem_bits(raw);
+        const uint32_t zp = penalised_bits<D>(z, RP);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          if (active[t] && in_range(t, zp)) push(t, id);
+        for (int t = 0; t < 2; ++t) {
+          if (!active[t]) continue;
+          const bool mem = in_range(t, zp);
+          // the packed count of the fast path took the id by its raw pattern
+          const int corr = (mem ? 1 : 0) - ((fast && in_range(t, z)) ? 1 : 0);
+          if (corr != 0) atomicAdd(&sh.slot[t][(id >> 3) / NT], static_cast<uint32_t>(corr));
+          if (mem) push(t, id);
+        }
       };
 #pragma unroll
       for (int k = 0; k < HPRE; ++k)
-        if (own[k]) hist_candidate(hpre[k], xh[k]);
+        if (own[k]) hist_candidate(hpre[k], xh2[k]);
       for (int i = tid + (hist_rows ? HPRE * NT : 0); i < H; i += NT) {
         if (!((sh.owner[i >> 5] >> (i & 31)) & 1u)) continue;
         const int id = hid[i];
@@ -858,76 +885,52 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
-      const int n = static_cast<int>(sh.nlist[t]);
-      if (n <= WAVE) {
-        // few candidates: wave 0 ranks them (indices are distinct) by counting
-        if (tid < WAVE) {
-          const uint32_t v = lane < n ? list[t][lane] : 0xFFFFFFFFu;
-          uint32_t below = 0;
-          for (int k = 0; k < n; ++k)
-            below += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), k)) < v ? 1u : 0u;
-          const uint64_t m = __ballot(lane < n && below == rank[t]);
-          if (m) {
-            const int res = __builtin_amdgcn_readlane(static_cast<int>(v), __ffsll(static_cast<unsigned long long>(m)) - 1);
-            if (tid == 0) sh.result[t] = res;
-          }
-        }
-      } else if (n <= LIST_CAP) {
-        // The member of rank r (by index): bucket counts over 128-index
-        // buckets locate the bucket holding rank r, and a 128-bit mask of
-        // that bucket's members gives the index.
-        uint32_t* bins = sh.hist + 2 * LIST_CAP;
-        for (int i = tid; i < RANK_BINS + 4; i += NT) bins[i] = 0;
-        if (tid == 0) sh.rank_bin = 0xFFFFFFFFu;
-        __syncthreads();
-        for (int i = tid; i < n; i += NT) atomicAdd(&bins[list[t][i] >> 7], 1u);
-        __syncthreads();
-        if (tid < WAVE) {
-          // wave 0: running counts over the buckets, 16 per lane
-          constexpr int PER = RANK_BINS / WAVE;
-          uint32_t c = 0;
+      const uint32_t n = sh.nh[t];
+      if (n <= static_cast<uint32_t>(HLIST_CAP)) {
+        // the slot holding rank r, then a block scan of the members each
+        // thread holds there (its chunk's non-history members and the listed
+        // history members in its chunk)
+        int js = -1;
+        uint32_t rr = 0, run = 0;
 #pragma unroll
-          for (int k = 0; k < PER; ++k) c += bins[tid * PER + k];
-          const uint32_t incl = wave_incl_scan(c);
-          const uint32_t excl = incl - c;
-          if (excl <= rank[t] && rank[t] < incl) {
-            uint32_t run = excl;
-            for (int k = 0; k < PER; ++k) {
-              const uint32_t bk = bins[tid * PER + k];
-              if (rank[t] < run + bk) {
-                sh.rank_bin = tid * PER + k;
-                sh.rank_in_bin = rank[t] - run;
-                break;
-              }
-              run += bk;
+        for (int j = 0; j < NCH; ++j) {
+          const uint32_t tj = sh.slot[t][j];
+          if (js < 0 && rank[t] < run + tj) {
+            js = j;
+            rr = rank[t] - run;
+          }
+          run += tj;
+        }
+        if (js >= 0) {  // the same in every thread
+          const int c = js * NT + tid;
+          uint32_t b = 0;
+          if (c < nchunks) {
+            uint4 q = make_uint4(0, 0, 0, 0);
+            if (fast) {
+#pragma unroll
+              for (int j = 0; j < NCH; ++j)
+                if (j == js) q = r[j];  // js is wave-uniform
+            } else {
+              q = load_chunk16(row, c, V, ALIGNED);
             }
+            b = chunk_mask(t, c, q);
+          }
+          for (uint32_t k = 0; k < n; ++k) {
+            const int id = static_cast<int>(hlist[t][k]);
+            if ((id >> 3) == c) b |= 1u << (id & 7);
+          }
+          const uint32_t cb = static_cast<uint32_t>(__popc(b));
+          uint32_t tot;
+          const uint32_t ex = block_excl_scan<uint32_t>(cb, sh.redu, &tot);
+          if (ex <= rr && rr < ex + cb) {
+            uint32_t m = b;
+            for (uint32_t q = ex; q < rr; ++q) m &= m - 1u;  // drop the lower members
+            sh.result[t] = c * 8 + (__ffs(m) - 1);
           }
         }
-        __syncthreads();
-        const uint32_t rb = sh.rank_bin;
-        uint32_t* mask = bins + RANK_BINS;  // 128 bits
-        for (int i = tid; i < n; i += NT) {
-          const uint32_t v = list[t][i];
-          if ((v >> 7) == rb) atomicOr(&mask[(v >> 5) & 3u], 1u << (v & 31u));
-        }
-        __syncthreads();
-        if (tid == 0) {
-          uint32_t need = sh.rank_in_bin;
-          for (int k = 0; k < 4; ++k) {
-            uint32_t m = mask[k];
-            const uint32_t pc = static_cast<uint32_t>(__popc(m));
-            if (need < pc) {
-              for (uint32_t q = 0; q < need; ++q) m &= m - 1u;  // drop the lowest `need` bits
-              sh.result[t] = static_cast<int32_t>(rb * 128u + 32u * k + (__ffs(m) - 1));
-              break;
-            }
-            need -= pc;
-          }
-        }
-        __syncthreads();
       } else {
-        // the candidate list overflowed: count matches round by round in
-        // index order (re-reads the row from memory; a rare path)
+        // the history member list overflowed: count members round by round
+        // in index order (re-reads the row from memory; a rare path)
         uint32_t base = 0;
         for (int j = 0; j < NCH; ++j) {
           const int e0 = (j * NT + tid) * 8;
@@ -953,8 +956,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
           base += tot;
           if (base > rank[t]) break;
         }
-        __syncthreads();
       }
+      __syncthreads();
     }
   }
   FL_MARK(8);

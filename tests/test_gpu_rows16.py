@@ -29,3 +29,72 @@ def test_hetero_bf16_parity(seed, B, V):
     print(summ)
     bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
     assert not bad, bad[:4]
+
+
+def _with_logits(w, x):
+    import dataclasses
+    return dataclasses.replace(w, logits=x)
+
+
+def test_ties_dense_bf16():
+    """Logits on a coarse grid: a few dozen distinct values, so the chosen
+    value's group has thousands of members (history ids among them), and the
+    member of rank r is found by slot counts and a block scan."""
+    print("[ties dense bf16] B=16 V=32000", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=5, batch=16, vocab=32000)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.round(torch.randn(16, 32000, generator=g) * 8.0) / 4.0).to(torch.bfloat16)
+    w = _with_logits(w, x)
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_vocab_50257_bf16(offset):
+    """V not a multiple of 8 (a partial last chunk); offset 1 makes the rows
+    unaligned (the path without the VGPR tile)."""
+    print(f"[vocab 50257 bf16] offset={offset}", flush=True)
+    B, V = 12, 50257
+    w = workloads.make("hetero_bf16_256x128256", seed=7, batch=B, vocab=V)
+    base = torch.zeros(B, V + 7, dtype=torch.bfloat16)
+    base[:, offset:offset + V] = w.logits
+    wd = w.to("cuda")
+    xd = base.to("cuda")[:, offset:offset + V]
+    assert xd.stride(0) == V + 7
+    out = sample_tokens(xd, return_logprobs=True, **wd.kwargs())
+    kw = wd.kwargs()
+    kw.pop("uniforms")
+    _, _, mask, status = filtered_outputs(xd, want_filtered=False, want_mask=True, **kw)
+    torch.cuda.synchronize()
+    assert int(status.abs().sum()) == 0
+    summ, verdicts = classify_workload(w, out.tokens, unpack_mask(mask, V))
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
+
+
+def test_hetero_f16():
+    print("[hetero f16] B=12 V=16384", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=3, batch=12, vocab=16384)
+    w = _with_logits(w, w.logits.float().to(torch.float16))
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
+
+
+def test_hetero_bf16_full_vocab():
+    print("[hetero bf16] B=8 V=128256", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=11, batch=8)
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
