@@ -16,7 +16,8 @@
 #include "../../include/fl_sampler.h"
 
 // Phase timestamps for kernel tuning builds (-DFL_PHASE_TIMES): thread 0 of
-// work-groups 0..3 records the constant-rate wall clock at each FL_MARK.
+// work-groups 0..3 records the constant-rate wall clock at each FL_MARK (and
+// every work-group its first and last mark).
 #ifdef FL_PHASE_TIMES
 // [0, 192): marks of blocks 0..3; [192, 192 + 2*1024): start / end of every block
 static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64 + 2 * 1024];
@@ -24,10 +25,7 @@ static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64 + 2 * 1024];
   do {                                                                          \
     if (threadIdx.x == 0) {                                                     \
       const uint64_t t_ = wall_clock64();                                       \
-      if (blockIdx.x < 4) {                                                     \
-        fl_phase_ts[blockIdx.x * 16 + (n)] = t_;                                \
-        fl_phase_ts[64 + blockIdx.x * 16 + (n)] = clock64();                    \
-      }                                                                         \
+      if (blockIdx.x < 4) fl_phase_ts[blockIdx.x * 16 + (n)] = t_;              \
       if (((n) == 0 || (n) == 9) && blockIdx.x < 1024)                          \
         fl_phase_ts[192 + 2 * blockIdx.x + ((n) == 9)] = t_;                    \
     }                                                                           \
@@ -52,8 +50,8 @@ struct BF16 {
   __device__ static __forceinline__ float to_f32(uint32_t b) { return __uint_as_float(b << 16); }
   __device__ static __forceinline__ uint32_t from_f32(float x) {
     const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // keep NaN a quiet NaN
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : rne;  // a NaN stays a quiet NaN
   }
   __device__ static __forceinline__ float rn(float x) { return to_f32(from_f32(x)); }
 };

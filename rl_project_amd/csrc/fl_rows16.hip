@@ -400,14 +400,16 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       x[SPW - 1] &= keep;
     }
     if (nan) atomicOr(&sh.status, FL_ROW_NAN);
-    // entries of step wave + 16k, held by lane k
-    uint32_t cv = 0;
+    // entries of step wave + 16k, held by lane k; bit k of `busy` marks a
+    // step with entries (wave-uniform)
+    uint32_t cv = 0, busy = 0;
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
       if (__ballot(x[k] != 0u) != 0) {
         const uint32_t c = static_cast<uint32_t>(__popcll(__ballot((x[k] & 0xFFFFu) != 0u)) +
                                                  __popcll(__ballot((x[k] >> 16) != 0u)));
         cv = (lane == k) ? c : cv;
+        busy |= 1u << k;
       }
     }
     if (lane < SPW) sh.stepc[wave + NWAVE * lane] = cv;
@@ -432,9 +434,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     const uint32_t spare = ENT_MAX + 2u * lane;
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
+      if (((busy >> k) & 1u) == 0) continue;
       const uint32_t a1 = x[k] & 0xFFFFu, a2 = x[k] >> 16;
       const uint64_t m1 = __ballot(a1 != 0u), m2 = __ballot(a2 != 0u);
-      if ((m1 | m2) == 0) continue;
       const uint32_t base =
           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(start), 2 * k + (wave >> 3)));
       const uint32_t below =
@@ -486,8 +488,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     uint32_t lc = 0;
     uint64_t lm = 0;
     for (int i = lo; i < hi; ++i) {
-      const uint32_t ord = ent[i] >> 16;
-      const float y = y_of_order<D, SC>(ord, CAP, T, sc_entry);
+      const uint32_t en = ent[i];
+      const float y = y_of_order<D, SC>(en >> 16, CAP, T, sc_entry);
       const float e = expf(y - M);
       if (cached) {
         Yc[i] = y;
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         Cc[i] = lc;  // prefix within the slice; the slice base is added below
         Cm[i] = lm;
       }
-      const uint32_t c = cnt_of(i);
+      const uint32_t c = en & 0xFFFFu;
       lc += c;
       lm += c * to_fx(e);
     }
@@ -713,11 +715,18 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         // entries before it
         uint64_t inner = 0;
         for (int j = s_lo + lane; j < is; j += WAVE) inner += kc(j) * qf(j);
-        const uint64_t cg = ex - wave_reduce(inner, OpAdd());
+        const uint64_t cg = ex - readlane64(wave_incl_scan(inner), WAVE - 1);
         const uint64_t q = qf(is);
         const uint32_t kept_g = kept_before(s_hi + 1) - kept_before(s_lo);
-        // member r of the group covers [cg + r q, cg + (r+1) q)
-        const uint64_t r = (q > 0 && target >= cg) ? (target - cg) / q : 0;
+        // member r of the group covers [cg + r q, cg + (r+1) q): r is the
+        // floor of (target - cg) / q, both below 2^53 (exact as doubles); the
+        // rounded quotient is at most one above the floor
+        uint64_t r = 0;
+        if (q > 0 && target >= cg) {
+          const uint64_t num = target - cg;
+          r = static_cast<uint64_t>(static_cast<double>(num) / static_cast<double>(q));
+          if (r * q > num) --r;
+        }
         if (tid == 0) {
           sh.dec.sel_rank = static_cast<uint32_t>(min(r, static_cast<uint64_t>(kept_g > 0 ? kept_g - 1 : 0)));
           sh.dec.y_sel = ys;
