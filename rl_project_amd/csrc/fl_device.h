@@ -21,9 +21,12 @@
 #ifdef FL_PHASE_TIMES
 // [0, 192): marks of blocks 0..3; [192, 192 + 2*1024): start / end of every block
 static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64 + 2 * 1024];
+#ifndef FL_MARK_MASK
+#define FL_MARK_MASK 0xFFFF  // marks recorded (bit n: FL_MARK(n)); fewer marks, fewer spills
+#endif
 #define FL_MARK(n)                                                              \
   do {                                                                          \
-    if (threadIdx.x == 0) {                                                     \
+    if (((FL_MARK_MASK >> (n)) & 1) && threadIdx.x == 0) {                      \
       const uint64_t t_ = wall_clock64();                                       \
       if (blockIdx.x < 4) fl_phase_ts[blockIdx.x * 16 + (n)] = t_;              \
       if (((n) == 0 || (n) == 9) && blockIdx.x < 1024)                          \

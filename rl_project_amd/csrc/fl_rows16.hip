@@ -191,7 +191,6 @@ __device__ __forceinline__ float exp_of_order(uint32_t order, float cap, float t
 template <class D, bool SC>
 __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN) {
   __shared__ Shared16 sh;
-  FL_MARK(0);
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int V = static_cast<int>(a.vocab);
@@ -231,7 +230,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // system accepts them (at the HBM rate), so a barrier placed after them
   // would only open once the whole row had arrived.  Straight-line stores: a
   // loop here makes the compiler wait for outstanding loads.
-  FL_MARK(10);
+  FL_MARK(0);  // (after the parameter loads: a mark before them makes the tuning build spill)
   static_assert(HIST_WORDS == 8 * 4 * NT && HBITS_WORDS == 4 * NT && OWNER_WORDS <= 4 * NT, "LDS clear layout");
 #pragma unroll
   for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(sh.hist)[tid + k * NT] = make_uint4(0, 0, 0, 0);
