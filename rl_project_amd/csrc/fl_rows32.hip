@@ -2,8 +2,32 @@
 //
 // One work-group of 1024 threads owns one row.  Float32 rows have too many
 // distinct values to histogram exactly, so each decision of the reference
-// sampler (src/forgeline/models/generation/sampling.py:26-61) is located by
-// radix narrowing on an order-preserving 32-bit key of the filtered value y:
+// sampler (src/forgeline/models/generation/sampling.py:26-61) is located in
+// value bins and settled element by element among the members of the bins
+// that hold a decision point.
+//
+// Two-read path (taken whenever it applies):
+//   read 1   anchors 4095 bins of width 1/64 on A = the largest value among
+//            the first 16384 elements (bin b holds values in about
+//            (A + 24 - (b+1)/64, A + 24 - b/64]; the last bin takes everything
+//            lower).  Each element adds one packed 64-bit word to its bin:
+//            count << 45 | round(exp(y - ub_b) * 2^26), a term relative to the
+//            bin's upper bound, so the row maximum is not needed yet.  After
+//            the read, M = max y is known and every bin's mass becomes
+//            exp(ub_b - M) * (its term sum) in 2^-45 fixed point.
+//   plan     the bin of each decision point is bounded from the bin prefix
+//            counts and masses alone (top-k by rank, min-p by the value where
+//            exp(y - M) >= min_p starts, top-p and the inverse CDF by mass,
+//            widened by the uncertainty of the cuts before them).
+//   read 2   gathers the members of those bins into LDS, sorts them by
+//            descending value then ascending index and settles each decision
+//            exactly; mass prefixes inside a bin use the same terms as the bin
+//            sums, so they meet the bin totals exactly.
+// Rows outside this envelope (a value more than 24 above A, a decision in the
+// last bin, more than CAP members to gather) take the multi-pass path below.
+//
+// Multi-pass path, by radix narrowing on an order-preserving 32-bit key of the
+// filtered value y:
 //
 //   max      a pass over the row finds M = max y (the softmax shift) and
 //            checks for NaN / +inf
@@ -34,7 +58,9 @@
 //
 // Every pass reads the row again: the first from HBM, later ones mostly from
 // L2 for rows of up to a few hundred KB.
+#include <cfloat>
 #include <climits>
+#include <type_traits>
 
 #include "fl_device.h"
 #include "fl_kernels.h"
@@ -51,6 +77,14 @@ constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;
 constexpr uint32_t KEY_MIN_FINITE = 0x00800000u;  // smallest key of a value above -inf
 constexpr int FXB = 45;                    // 2^-45 fixed point: 2^18 unit terms fit in 64 bits
 
+// Two-read path
+constexpr int NBF = 4096;                  // value bins; bin NBF-1 takes every lower value
+constexpr float BPU = 64.0f;               // bins per unit of filtered value
+constexpr float ANCHOR_UP = 24.0f;         // bin 0 starts this far above the anchor
+constexpr int CNT_SH = 45;                 // bin word: count << 45 | sum of 2^-26 terms
+constexpr uint64_t TERM_MASK = (1ull << CNT_SH) - 1u;
+constexpr int NRANGE = 4;                  // bin ranges gathered by the second read
+
 // e in [0, 1] as fixed point round(e * 2^45) (halves rounded up).
 __device__ __forceinline__ uint64_t fx45(float e) {
   const uint32_t u = __float_as_uint(e);
@@ -65,11 +99,27 @@ __device__ __forceinline__ uint64_t fx45(float e) {
 __device__ __forceinline__ double from_fx45(uint64_t v) { return static_cast<double>(v) * (1.0 / 35184372088832.0); }
 
 struct Shared32 {
-  uint32_t cnt1[NB];   // level-1 bins, kept for every decision
-  uint64_t mass1[NB];
-  uint32_t cnt[NB];    // deeper levels
-  uint64_t mass[NB];
+  union {
+    struct {
+      uint32_t cnt1[NB];   // level-1 bins, kept for every decision
+      uint64_t mass1[NB];
+      uint32_t cnt[NB];    // deeper levels
+      uint64_t mass[NB];
+    };
+    struct {
+      uint64_t acc[NBF + 1];  // two-read bins: packed sums, then exclusive mass prefixes; [NBF]: discard slot
+      uint32_t pc[NBF];    // exclusive count prefixes
+    };
+  };
   uint64_t cand[CAP];  // (key << 32) | ~index, sorted descending
+  uint64_t cscan[CAP]; // two-read path: inclusive mass prefix at each candidate
+  int32_t rlo[NRANGE], rhi[NRANGE], rbase[NRANGE];
+  int32_t fplan[8];
+  float xlo[2][NRANGE], xhi[2][NRANGE];
+  uint32_t fkey[2];
+  uint64_t fmass_out;
+  uint64_t fck;
+  int64_t ftok;
   uint64_t redq[NWAVE];
   uint32_t redu[NWAVE];
   int32_t redi[NWAVE];
@@ -128,10 +178,10 @@ struct Xform {
 // pass streams the row from HBM, later passes of a row of up to a few hundred
 // KB mostly hit L2.  Called by all threads (block-uniform control flow).
 template <class F>
-__device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f) {
+__device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f, int from = 0) {
   const int tid = threadIdx.x;
   const int nch = X.nch;
-  for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
+  for (int c0 = from; c0 < nch; c0 += 4 * NT) {
     float4 q[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
@@ -147,6 +197,54 @@ __device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f) {
       }
       // one chunk's elements at a time (interleaving all 16 costs VGPRs)
       __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// f(idx, x, hist, valid) for every element: the raw logit and its history bit.
+template <class F>
+__device__ __forceinline__ void row_pass_raw(const Src& S, const Xform& X, F&& f) {
+  const int tid = threadIdx.x;
+  const int nch = X.nch;
+  for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * NT + tid;
+      const uint32_t hb = X.nibble(c);
+      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int idx = 4 * c + e;
+        f(idx, xs[e], ((hb >> e) & 1u) != 0u, idx < S.V);
+      }
+    }
+  }
+}
+
+// First key k in [a, b) with pred(k) true, for a predicate that is false then
+// true along the range (b if it never holds); 64 probes per step, as
+// wave_first, over the 32-bit key range.
+template <class P>
+__device__ __forceinline__ uint32_t wave_first_key(uint32_t a, uint32_t b, P&& pred) {
+  const uint64_t lane = threadIdx.x & (WAVE - 1);
+  uint64_t lo = a, hi = b;
+  for (;;) {
+    if (hi <= lo) return static_cast<uint32_t>(hi);
+    const uint64_t n = hi - lo;
+    const uint64_t s = n >= WAVE ? (n + WAVE - 1) / WAVE : 1u;
+    const uint64_t p = lo + lane * s;
+    const uint64_t m = __ballot(p < hi && pred(static_cast<uint32_t>(p)));
+    if (s == 1) return m ? static_cast<uint32_t>(lo + __ffsll(static_cast<unsigned long long>(m)) - 1) : static_cast<uint32_t>(hi);
+    if (m == 0) {
+      lo += min<uint64_t>(WAVE - 1, (n - 1) / s) * s + 1;
+    } else {
+      const uint64_t f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+      if (f == 0) return static_cast<uint32_t>(lo);
+      hi = lo + f * s;
+      lo = lo + (f - 1) * s + 1;
     }
   }
 }
@@ -276,6 +374,519 @@ struct Narrow {
   int n;              // candidates gathered (OUT_CAND)
 };
 
+// ------------------------------------------------------------ two-read path
+struct OpOr { template <typename T> __device__ T operator()(T a, T b) const { return a | b; } };
+
+// Bin of a value y <= c (c = anchor + ANCHOR_UP): floor((c - y) * 64), the
+// last bin for everything lower (-inf included); values above c give 0 or -1.
+// Non-increasing in y, so the bins cut the value order into contiguous ranges.
+__device__ __forceinline__ int fbin(float y, float c) {
+  return static_cast<int>(fminf(fmaxf((c - y) * BPU, -1.0f), static_cast<float>(NBF - 1)));
+}
+// Upper bound of bin b's values (up to rounding).
+__device__ __forceinline__ float fub(int b, float c) { return c - static_cast<float>(b) * (1.0f / BPU); }
+// round(exp(y - ub_b) * 2^26) for y in bin b; y - ub_b lies in about
+// [-1/64, 0], where the degree-4 Taylor polynomial is exact to 1e-11, and
+// t * 2^26 < 2^27 is an integer (t has 24 significant bits).  The last bin
+// adds no mass: its values lie more than 40 below the anchor, so their
+// weights are below e^-40 of the largest.
+__device__ __forceinline__ uint32_t fterm(float y, int b, float c) {
+  const float d = fminf(y - fub(b, c), 0.0625f);
+  const float t = fmaf(d, fmaf(d, fmaf(d, fmaf(d, 1.0f / 24.0f, 1.0f / 6.0f), 0.5f), 1.0f), 1.0f);
+  return b == NBF - 1 ? 0u : static_cast<uint32_t>(t * 67108864.0f);
+}
+// Mass in 2^-45 fixed point relative to M of term sum F (2^-26 units) in bin b:
+// round(F * exp(ub_b - M) * 2^19).  Bin totals and in-bin prefixes both use it,
+// so the prefixes of a bin end exactly at its total.
+__device__ __forceinline__ uint64_t fmass(uint64_t F, int b, float c, float M) {
+  if (F == 0) return 0;
+  const double g = exp(static_cast<double>(fub(b, c)) - static_cast<double>(M)) * 524288.0;
+  return static_cast<uint64_t>(static_cast<double>(F) * g + 0.5);
+}
+
+struct RowCfg {
+  int V, K;
+  float T, TP, MP, U;
+  bool select;
+};
+struct RowOut {
+  uint32_t kmax;
+  int32_t status;
+  uint32_t tau;
+  uint64_t CK;
+  uint64_t keep_mass;
+  uint32_t keep_n;
+  int64_t tok;
+};
+
+// The two-read path.  Returns false, with nothing decided, when the row needs
+// the multi-pass path.  Called by all threads (block-uniform control flow).
+__device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform& X, const RowCfg& R, RowOut& o) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (WAVE - 1);
+  const int V = R.V;
+  o.kmax = 0;
+  o.status = 0;
+  o.tau = KEY_MIN_FINITE;
+  o.CK = static_cast<uint64_t>(KEY_MIN_FINITE) << 32;
+  o.keep_mass = 0;
+  o.keep_n = 0;
+  o.tok = -1;
+
+  // ---------------------------------------------- read 1
+  for (int i = tid; i < NBF; i += NT) sh.acc[i] = 0;
+  float yb[16];
+  {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = u * NT + tid;
+      const uint32_t hb = X.nibble(c);
+      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) yb[4 * u + e] = X.y(xs[e], (hb >> e) & 1u);
+    }
+  }
+  uint32_t km = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int idx = 4 * ((j >> 2) * NT + tid) + (j & 3);
+    if (idx < V && yb[j] == yb[j]) km = max(km, f32_key(yb[j]));
+  }
+  const uint32_t ka = block_reduce<uint32_t>(km, OpMax(), sh.redu);  // also orders the bin clearing
+  const float A = f32_of_key(ka);
+  if (!(ka > KEY_NEG_INF && ka < KEY_POS_INF && fabsf(A) < 1048576.0f)) return false;
+  const float c = A + ANCHOR_UP;
+
+  uint32_t nfin = 0;
+  uint32_t bad = 0;  // 1: a value above the bins, 2: NaN
+  // branch-free: an element outside the bins adds 0 to the discard slot
+  auto add = [&](int idx, float y) __attribute__((always_inline)) {
+    const bool valid = idx < V;
+    bad |= (valid && y != y) ? 2u : 0u;
+    bad |= (valid && y > c) ? 1u : 0u;
+    const bool ok = valid && y <= c;
+    km = max(km, ok ? f32_key(y) : 0u);
+    nfin += (ok && y > -__builtin_inff()) ? 1u : 0u;
+    const int b = fbin(y, c);
+    const uint64_t w = (1ull << CNT_SH) | fterm(y, b, c);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&sh.acc[ok ? b : NBF]),
+              static_cast<unsigned long long>(ok ? w : 0ull));
+  };
+#pragma unroll
+  for (int j = 0; j < 16; ++j) add(4 * ((j >> 2) * NT + tid) + (j & 3), yb[j]);
+  row_pass(S, X, [&](int idx, float y, bool) { add(idx, y); }, 4 * NT);
+  const uint32_t kmx = block_reduce<uint32_t>(km, OpMax(), sh.redu);
+  const uint32_t bad_all = block_reduce<uint32_t>(bad, OpOr(), sh.redu);
+  const uint32_t nf = block_reduce<uint32_t>(nfin, OpAdd(), sh.redu);
+  int32_t status = sh.status;
+  if (bad_all & 2u) status |= FL_ROW_NAN;
+  else if (bad_all & 1u) {
+    // +inf values are above every bin
+    if (status == 0) return false;
+  }
+  o.kmax = kmx;
+  o.status = status;
+  if (status != 0) return true;
+  const float M = f32_of_key(kmx);
+
+  // ---------------------------------------------- bin prefixes
+  uint32_t tc;
+  uint64_t tm;
+  {
+    uint32_t cb[4];
+    uint64_t mb[4];
+    uint32_t lc = 0;
+    uint64_t lm = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = 4 * tid + j;
+      const uint64_t w = sh.acc[b];
+      cb[j] = static_cast<uint32_t>(w >> CNT_SH);
+      mb[j] = fmass(w & TERM_MASK, b, c, M);
+      lc += cb[j];
+      lm += mb[j];
+    }
+    uint32_t ec;
+    uint64_t em;
+    block_excl_scan2(lc, lm, sh.redu, sh.redq, ec, em, tc, tm);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = 4 * tid + j;
+      sh.pc[b] = ec;
+      sh.acc[b] = em;
+      ec += cb[j];
+      em += mb[j];
+    }
+  }
+  __syncthreads();
+  auto Pn = [&](int b) -> uint32_t { return b < NBF ? sh.pc[b] : tc; };
+  auto Qm = [&](int b) -> uint64_t { return b < NBF ? sh.acc[b] : tm; };
+
+  const bool tk_on = R.K > 0 && R.K < V;
+  const bool mp_on = R.MP > 0.0f;
+  const bool tp_on = R.TP > 0.0f && R.TP < 1.0f;
+
+  // ---------------------------------------------- plan (wave 0)
+  // fplan: 0 ok, 1 status, 2 bk, 3 bc, 4 ranges, 5 gathered count
+  if (tid < WAVE) {
+    int ok = 1;
+    int32_t st = 0;
+    int bk = NBF, bm = NBF;
+    uint32_t kp = 0;
+    if (tk_on) bk = wave_first(0, NBF, [&](int b) { return Pn(b + 1) > static_cast<uint32_t>(R.K - 1); });
+    if (mp_on) {
+      if (!(1.0f >= R.MP)) {
+        st |= FL_ROW_ALL_MASKED;  // min_p > 1 removes every value
+      } else {
+        // smallest key whose value passes exp(y - M) >= min_p (kmx passes)
+        auto pass = [&](uint32_t k) { return expf(f32_of_key(k) - M) >= R.MP; };
+        uint32_t lo = KEY_MIN_FINITE, hi = kmx;
+        if (pass(lo)) {
+          kp = lo;
+        } else {
+          while (hi - lo > 1u) {
+            const uint32_t mid = lo + (hi - lo) / 2u;
+            if (pass(mid)) hi = mid;
+            else lo = mid;
+          }
+          kp = hi;
+        }
+        bm = fbin(f32_of_key(kp), c);
+      }
+    }
+    const int bc = min(bk, bm);  // bin of the binding value cut (NBF: none)
+    if (bc == NBF - 1) ok = 0;
+    int lo_[NRANGE], hi_[NRANGE];
+    int nr = 0;
+    if (bc < NBF) {
+      lo_[nr] = bc;
+      hi_[nr] = bc;
+      ++nr;
+    }
+    uint64_t kmlo = tm, kmhi = tm;  // bounds of the mass kept by the value cuts
+    if (bc < NBF) {
+      kmlo = Qm(bc);
+      kmhi = Qm(bc + 1);
+    }
+    int blast = bc < NBF ? bc : NBF - 1;  // last bin holding kept values
+    uint64_t k2lo = kmlo, k2hi = kmhi;
+    if (tp_on) {
+      const uint64_t tlo = static_cast<uint64_t>(ceil(static_cast<double>(R.TP) * static_cast<double>(kmlo)));
+      const uint64_t thi = static_cast<uint64_t>(ceil(static_cast<double>(R.TP) * static_cast<double>(kmhi)));
+      const int plo = min(blast, wave_first(0, NBF, [&](int b) { return Qm(b + 1) >= tlo; }));
+      const int phi = min(blast, wave_first(0, NBF, [&](int b) { return Qm(b + 1) >= thi; }));
+      if (phi >= NBF - 1) ok = 0;
+      lo_[nr] = plo;
+      hi_[nr] = phi;
+      ++nr;
+      // the kept mass ends at the crossing member: at least thr, at most the
+      // inclusive mass of its bin
+      k2lo = tlo;
+      k2hi = min(kmhi, Qm(phi + 1));
+      blast = phi;
+    }
+    if (R.select) {
+      int s0, s1;
+      if (R.T > 0.0f) {
+        const uint64_t tlo = static_cast<uint64_t>(floor(static_cast<double>(R.U) * static_cast<double>(k2lo)));
+        const uint64_t thi = static_cast<uint64_t>(floor(static_cast<double>(R.U) * static_cast<double>(k2hi)));
+        s0 = min(blast, wave_first(0, NBF, [&](int b) { return Qm(b + 1) > tlo; }));
+        s1 = min(blast, wave_first(0, NBF, [&](int b) { return Qm(b + 1) > thi; }));
+      } else {
+        s0 = s1 = wave_first(0, NBF, [&](int b) { return Pn(b + 1) > 0u; });  // the maximum's bin
+      }
+      if (s1 >= NBF - 1) ok = 0;
+      lo_[nr] = s0;
+      hi_[nr] = s1;
+      ++nr;
+    }
+    // sort the ranges by their first bin and merge overlapping or adjacent ones
+    for (int i = 1; i < nr; ++i)
+      for (int j = i; j > 0 && lo_[j] < lo_[j - 1]; --j) {
+        const int tl = lo_[j], th = hi_[j];
+        lo_[j] = lo_[j - 1];
+        hi_[j] = hi_[j - 1];
+        lo_[j - 1] = tl;
+        hi_[j - 1] = th;
+      }
+    int m = 0;
+    for (int i = 0; i < nr; ++i) {
+      if (m > 0 && lo_[i] <= hi_[m - 1] + 1) {
+        hi_[m - 1] = max(hi_[m - 1], hi_[i]);
+      } else {
+        lo_[m] = lo_[i];
+        hi_[m] = hi_[i];
+        ++m;
+      }
+    }
+    uint32_t total = 0;
+    for (int i = 0; i < m; ++i) {
+      if (lane == 0) {
+        sh.rlo[i] = lo_[i];
+        sh.rhi[i] = hi_[i];
+        sh.rbase[i] = static_cast<int32_t>(total);
+      }
+      total += Pn(hi_[i] + 1) - Pn(lo_[i]);
+    }
+    if (total > static_cast<uint32_t>(CAP)) ok = 0;
+    if (lane == 0) {
+      for (int i = m; i < NRANGE; ++i) {
+        sh.rlo[i] = 1;
+        sh.rhi[i] = 0;
+        sh.rbase[i] = 0;
+      }
+      sh.fplan[0] = ok;
+      sh.fplan[1] = st;
+      sh.fplan[2] = bk;
+      sh.fplan[3] = bc;
+      sh.fplan[4] = m;
+      sh.fplan[5] = static_cast<int32_t>(total);
+      sh.fplan[6] = bm;
+      sh.fkey[0] = kp;
+      sh.ncand = 0;
+    }
+  }
+  __syncthreads();
+  const int32_t st = sh.fplan[1];
+  if (st != 0) {
+    o.status = st;
+    return true;
+  }
+  if (!sh.fplan[0]) return false;
+  const int bk = sh.fplan[2], bc = sh.fplan[3], nr = sh.fplan[4], ngath = sh.fplan[5], bm = sh.fplan[6];
+  const uint32_t kp = sh.fkey[0];
+  int rl[NRANGE], rh[NRANGE], rb[NRANGE];
+#pragma unroll
+  for (int i = 0; i < NRANGE; ++i) {
+    rl[i] = sh.rlo[i];
+    rh[i] = sh.rhi[i];
+    rb[i] = sh.rbase[i];
+  }
+  auto gathered = [&](int b) {
+    bool in = false;
+#pragma unroll
+    for (int i = 0; i < NRANGE; ++i) in |= b >= rl[i] && b <= rh[i];
+    return in;
+  };
+  // index of bin b's first member among the candidates (b gathered)
+  auto cstart = [&](int b) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < NRANGE; ++i)
+      if (b >= rl[i] && b <= rh[i]) s = rb[i] + static_cast<int>(Pn(b) - Pn(rl[i]));
+    return s;
+  };
+
+  uint32_t tau = KEY_MIN_FINITE;
+  uint64_t CK = static_cast<uint64_t>(tau) << 32;
+  uint32_t keep_n = nf;
+  uint64_t keep_mass = tm;
+  int64_t tok = -1;
+  if (nr > 0) {
+    // ---------------------------------------------- read 2
+    // y is non-decreasing in the raw logit x within each class (history
+    // members or not), so the values of a bin range come from one interval
+    // of x per class.  One wave per interval end finds it by a 64-way search
+    // over the float order; the second read then stages only the elements
+    // whose raw logit lies in an interval, and y is evaluated for those alone.
+    // A non-monotone rounding would lose members, which the count check below
+    // catches (the row then takes the multi-pass path).
+    {
+      const int w = tid / WAVE;
+      const int nb = 2 * nr * (X.pen ? 2 : 1);
+      if (w < nb) {
+        const int r = (w >> 1) % nr;
+        const bool hist = w >= 2 * nr;
+        const bool upper = w & 1;
+        auto bin_of_x = [&](uint32_t kx) { return fbin(X.y(f32_of_key(kx), hist), c); };
+        // finite x only: +-inf map to +-inf (a non-finite y is never gathered)
+        const uint32_t k0 = f32_key(-FLT_MAX), k1 = f32_key(FLT_MAX) + 1u;
+        uint32_t k;
+        if (!upper) {
+          k = wave_first_key(k0, k1, [&](uint32_t kx) { return bin_of_x(kx) <= rh[r]; });
+        } else {
+          k = wave_first_key(k0, k1, [&](uint32_t kx) { return bin_of_x(kx) < rl[r]; });
+        }
+        if (lane == 0) {
+          // empty interval: lower end +inf or upper end -inf
+          if (!upper) sh.xlo[hist][r] = k == k1 ? __builtin_inff() : f32_of_key(k);
+          else sh.xhi[hist][r] = k == k0 ? -__builtin_inff() : f32_of_key(k - 1u);
+        }
+      }
+      __syncthreads();
+    }
+    // interval ends of the plain (0) and history (1) classes; unused ranges empty
+    float xl0[NRANGE], xh0[NRANGE], xl1[NRANGE], xh1[NRANGE];
+#pragma unroll
+    for (int i = 0; i < NRANGE; ++i) {
+      xl0[i] = i < nr ? sh.xlo[0][i] : __builtin_inff();
+      xh0[i] = i < nr ? sh.xhi[0][i] : -__builtin_inff();
+      xl1[i] = i < nr && X.pen ? sh.xlo[1][i] : __builtin_inff();
+      xh1[i] = i < nr && X.pen ? sh.xhi[1][i] : -__builtin_inff();
+    }
+    auto stage = [&](auto pen_tag) __attribute__((always_inline)) {
+      row_pass_raw(S, X, [&](int idx, float x, bool hist, bool valid) {
+        bool in = false;
+#pragma unroll
+        for (int i = 0; i < NRANGE; ++i) in |= x >= xl0[i] && x <= xh0[i];
+        if constexpr (decltype(pen_tag)::value) {
+          bool inh = false;
+#pragma unroll
+          for (int i = 0; i < NRANGE; ++i) inh |= x >= xl1[i] && x <= xh1[i];
+          in = hist ? inh : in;
+        }
+        wave_append(valid && in,
+                    (static_cast<uint64_t>(__float_as_uint(x)) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(idx)),
+                    &sh.ncand, sh.cand);
+      });
+    };
+    if (X.pen) stage(std::true_type{});
+    else stage(std::false_type{});
+    __syncthreads();
+    const int ns = static_cast<int>(sh.ncand);
+    if (ns > CAP) return false;
+    // staged raw logits -> candidates (key << 32 | ~index); non-members -> 0
+    uint32_t nm = 0;
+    for (int i = tid; i < ns; i += NT) {
+      const uint64_t v = sh.cand[i];
+      const int idx = static_cast<int>(~static_cast<uint32_t>(v));
+      const float y = X.y(__uint_as_float(static_cast<uint32_t>(v >> 32)), (X.nibble(idx >> 2) >> (idx & 3)) & 1u);
+      const bool mem = y <= c && gathered(fbin(y, c));
+      nm += mem ? 1u : 0u;
+      sh.cand[i] = mem ? (static_cast<uint64_t>(f32_key(y)) << 32) | (v & 0xFFFFFFFFull) : 0ull;
+    }
+    nm = block_reduce<uint32_t>(nm, OpAdd(), sh.redu);
+    if (nm != static_cast<uint32_t>(ngath)) return false;
+    bitonic_desc(sh.cand, ns);  // members first (every member word is nonzero)
+    const int n = ngath;
+
+    // inclusive mass prefix at each candidate
+    {
+      uint64_t f[4];
+      int bb[4];
+      uint64_t ls = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        f[j] = 0;
+        bb[j] = 0;
+        if (i < n) {
+          const float y = f32_of_key(static_cast<uint32_t>(sh.cand[i] >> 32));
+          bb[j] = fbin(y, c);
+          f[j] = fterm(y, bb[j], c);
+          ls += f[j];
+        }
+      }
+      uint64_t tot;
+      uint64_t run = block_excl_scan<uint64_t>(ls, sh.redq, &tot);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        run += f[j];
+        if (i < n) sh.cscan[i] = run;
+      }
+      __syncthreads();
+      uint64_t incl[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        incl[j] = 0;
+        if (i < n) {
+          const int h = cstart(bb[j]);
+          const uint64_t F = sh.cscan[i] - (h > 0 ? sh.cscan[h - 1] : 0ull);
+          incl[j] = Qm(bb[j]) + fmass(F, bb[j], c, M);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        if (i < n) sh.cscan[i] = incl[j];
+      }
+      __syncthreads();
+    }
+
+    // ---------------------------------------------- decisions (wave 0)
+    if (tid < WAVE) {
+      int ok = 1;
+      int32_t st2 = 0;
+      auto key_at = [&](int i) { return static_cast<uint32_t>(sh.cand[i] >> 32); };
+      if (bc < NBF) {
+        // value cuts: top-k keeps y >= the K-th largest, min-p keeps keys >= kp
+        if (tk_on && bk == bc) tau = max(tau, key_at(cstart(bk) + (R.K - 1 - static_cast<int>(Pn(bk)))));
+        if (mp_on && bm == bc) tau = max(tau, kp);
+        const int h = cstart(bc), cnt = static_cast<int>(Pn(bc + 1) - Pn(bc));
+        const int ck = wave_first(h, h + cnt, [&](int i) { return key_at(i) < tau; }) - h;
+        keep_n = Pn(bc) + static_cast<uint32_t>(ck);
+        keep_mass = ck > 0 ? sh.cscan[h + ck - 1] : Qm(bc);
+      }
+      CK = static_cast<uint64_t>(tau) << 32;
+      if (keep_n == 0 || tau > o.kmax) st2 |= FL_ROW_ALL_MASKED;
+      if (st2 == 0 && tp_on) {
+        // first position whose inclusive mass reaches thr; it and all before are kept
+        const uint64_t thr = static_cast<uint64_t>(ceil(static_cast<double>(R.TP) * static_cast<double>(keep_mass)));
+        const int bp = wave_first(0, NBF, [&](int b) { return Qm(b + 1) >= thr; });
+        if (bp >= NBF || !gathered(bp)) {
+          ok = 0;
+        } else {
+          const int h = cstart(bp), cnt = static_cast<int>(Pn(bp + 1) - Pn(bp));
+          const int j = wave_first(h, h + cnt, [&](int i) { return sh.cscan[i] >= thr; });
+          if (j >= h + cnt) {
+            ok = 0;
+          } else {
+            CK = sh.cand[j];
+            keep_n = Pn(bp) + static_cast<uint32_t>(j - h) + 1u;
+            keep_mass = sh.cscan[j];
+          }
+        }
+      }
+      if (st2 == 0 && ok && R.select) {
+        if (R.T > 0.0f) {
+          const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(R.U) * static_cast<double>(keep_mass)));
+          const int bs = wave_first(0, NBF, [&](int b) { return Qm(b + 1) > target; });
+          if (bs >= NBF || !gathered(bs)) {
+            ok = 0;
+          } else {
+            const int h = cstart(bs), cnt = static_cast<int>(Pn(bs + 1) - Pn(bs));
+            const int j = wave_first(h, h + cnt, [&](int i) { return sh.cscan[i] > target; });
+            if (j >= h + cnt || Pn(bs) + static_cast<uint32_t>(j - h) >= keep_n) ok = 0;
+            else tok = static_cast<uint32_t>(~static_cast<uint32_t>(sh.cand[j]));
+          }
+        } else {
+          tok = static_cast<uint32_t>(~static_cast<uint32_t>(sh.cand[0]));  // first index of the maximum
+        }
+      }
+      if (lane == 0) {
+        sh.fplan[0] = ok;
+        sh.fplan[1] = st2;
+        sh.fkey[1] = tau;
+        sh.fplan[7] = static_cast<int32_t>(keep_n);
+        sh.fmass_out = keep_mass;
+        sh.ftok = tok;
+        sh.fck = CK;
+      }
+    }
+    __syncthreads();
+    if (!sh.fplan[0]) return false;
+    o.status = sh.fplan[1];
+    tau = sh.fkey[1];
+    keep_n = static_cast<uint32_t>(sh.fplan[7]);
+    keep_mass = sh.fmass_out;
+    tok = sh.ftok;
+    CK = sh.fck;
+    __syncthreads();
+  }
+  o.tau = tau;
+  o.CK = CK;
+  o.keep_n = keep_n;
+  o.keep_mass = keep_mass;
+  o.tok = tok;
+  return true;
+}
+
 }  // namespace
 
 __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
@@ -327,11 +938,21 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   Xform X;
   X.cap = a.softcap;
   X.rp = RP;
-  X.t = T;
+  X.t = T == 1.0f ? 0.0f : T;  // x / 1 == x exactly: skip the division
   X.pen = pen;
   X.hbits = hbits_dyn;
   X.nch = nch;
 
+  RowCfg R;
+  R.V = V;
+  R.K = K;
+  R.T = T;
+  R.TP = TP;
+  R.MP = MP;
+  R.U = U;
+  R.select = select;
+  RowOut o;
+  if (!two_read(sh, S, X, R, o)) {
   // ------------------------------------------------ first read: max, NaN
   uint32_t kmax = 0;
   int nan = 0;
@@ -716,7 +1337,21 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
     if (stage == 3 && tok < 0) status |= FL_ROW_LIMIT;
   }
 
-  const double SK = from_fx45(keep_mass);
+  o.kmax = kmax;
+  o.status = status;
+  o.tau = tau;
+  o.CK = CK;
+  o.keep_mass = keep_mass;
+  o.keep_n = keep_n;
+  o.tok = tok;
+  }  // multi-pass path
+
+  const float M = f32_of_key(o.kmax);
+  int32_t status = o.status;
+  int64_t tok = o.tok;
+  const uint64_t CK = o.CK;
+  const uint32_t keep_n = o.keep_n;
+  const double SK = from_fx45(o.keep_mass);
   const float rK = 1.0f / static_cast<float>(SK);
   float y_sel = 0.0f;
   if (tid == 0 && status == 0 && tok >= 0) {

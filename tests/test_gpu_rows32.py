@@ -55,3 +55,53 @@ def test_hetero_f32_parity(seed, B, V):
     print(f"[hetero f32] seed={seed} B={B} V={V}", flush=True)
     w = workloads.make("hetero_bf16_256x128256", seed=seed, batch=B, vocab=V)
     _check(dataclasses.replace(w, logits=w.logits.float()))
+
+
+def _with(w, **kw):
+    return dataclasses.replace(w, **kw)
+
+
+def test_ascending_rows_f32():
+    """Values rising along the row: most lie above the bins anchored on the
+    row's first elements, so these rows take the multi-pass path."""
+    B, V = 4, 65536
+    w = workloads.make("uniform_f32_64x32000", seed=7, batch=B, vocab=V)
+    x = torch.linspace(-60.0, 60.0, V).repeat(B, 1) + 0.01 * torch.randn(B, V, generator=torch.Generator().manual_seed(7))
+    print(f"[ascending f32] B={B} V={V}", flush=True)
+    _check(_with(w, logits=x.contiguous()))
+
+
+def test_integer_ties_f32():
+    """Integer logits: each value is one bin holding thousands of members, more
+    than the two-read path gathers, and exact ties at every cut."""
+    B, V = 8, 50000
+    g = torch.Generator().manual_seed(8)
+    w = workloads.make("uniform_f32_64x32000", seed=8, batch=B, vocab=V)
+    x = torch.round(torch.randn(B, V, generator=g) * 2.0)
+    print(f"[integer ties f32] B={B} V={V}", flush=True)
+    _check(_with(w, logits=x))
+
+
+def test_cold_topk_f32():
+    """Temperature 0.05 with top-k 200 spreads the kept values over hundreds
+    of units, so the k-th value falls below the bins of the two-read path."""
+    B, V = 6, 32000
+    w = workloads.make("uniform_f32_64x32000", seed=9, batch=B, vocab=V)
+    print(f"[cold top-k f32] B={B} V={V}", flush=True)
+    _check(_with(w, temperature=torch.full((B,), 0.05), top_k=torch.full((B,), 200, dtype=torch.int32),
+                 min_p=torch.zeros(B), top_p=torch.ones(B)))
+
+
+@pytest.mark.parametrize("case", ["greedy", "nofilter", "minp_only", "topk1"])
+def test_param_edges_f32(case):
+    B, V = 8, 40000
+    w = workloads.make("uniform_f32_64x32000", seed=10, batch=B, vocab=V)
+    kw = dict(top_k=torch.zeros(B, dtype=torch.int32), top_p=torch.ones(B), min_p=torch.zeros(B))
+    if case == "greedy":
+        kw = dict(temperature=torch.zeros(B))
+    elif case == "minp_only":
+        kw["min_p"] = torch.tensor([0.0, 0.01, 0.1, 0.5, 1.0, 0.3, 0.05, 0.9])
+    elif case == "topk1":
+        kw["top_k"] = torch.ones(B, dtype=torch.int32)
+    print(f"[param edges f32] {case} B={B} V={V}", flush=True)
+    _check(_with(w, **kw))
