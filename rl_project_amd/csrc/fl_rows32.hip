@@ -168,6 +168,16 @@ struct Xform {
     // + 0.0f turns -0 into +0: the filters compare -0 == +0, so both get one key
     return temperature_val<F32>(z, t) + 0.0f;
   }
+  // y with the row's uniform choices fixed at compile time: TDIV = t > 0
+  // (a division by the temperature), PEN = pen.  Equal to y() bit for bit.
+  template <bool TDIV, bool PEN>
+  __device__ __forceinline__ float yt(float x, bool hist) const {
+    float z = x;
+    if (cap > 0.0f) z = softcap_val<F32>(z, cap);
+    if (PEN && hist) z = penalty_val<F32>(z, rp);
+    if (TDIV) z = F32::rn(z / t);
+    return z + 0.0f;
+  }
   // history bits of elements 4c .. 4c+3
   __device__ __forceinline__ uint32_t nibble(int c) const {
     return (pen && c < nch) ? (hbits[c >> 3] >> ((c & 7) * 4)) & 0xFu : 0u;
@@ -419,21 +429,13 @@ struct RowOut {
   int64_t tok;
 };
 
-// The two-read path.  Returns false, with nothing decided, when the row needs
-// the multi-pass path.  Called by all threads (block-uniform control flow).
-__device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform& X, const RowCfg& R, RowOut& o) {
+// Read 1 of the two-read path: anchor the bins on the largest value among the
+// first 4 chunks per thread, then add every element to its bin.  Returns false
+// (uniformly) when the anchor is not a finite value below 2^20 in magnitude.
+template <bool TDIV, bool PEN>
+__device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X, int V, float& c, uint32_t& km,
+                                      uint32_t& nfin, uint32_t& bad) {
   const int tid = threadIdx.x;
-  const int lane = tid & (WAVE - 1);
-  const int V = R.V;
-  o.kmax = 0;
-  o.status = 0;
-  o.tau = KEY_MIN_FINITE;
-  o.CK = static_cast<uint64_t>(KEY_MIN_FINITE) << 32;
-  o.keep_mass = 0;
-  o.keep_n = 0;
-  o.tok = -1;
-
-  // ---------------------------------------------- read 1
   for (int i = tid; i < NBF; i += NT) sh.acc[i] = 0;
   float yb[16];
   {
@@ -442,14 +444,13 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     for (int u = 0; u < 4; ++u) q[u] = S.chunk(u * NT + tid);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int c = u * NT + tid;
-      const uint32_t hb = X.nibble(c);
+      const int ch = u * NT + tid;
+      const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) yb[4 * u + e] = X.y(xs[e], (hb >> e) & 1u);
+      for (int e = 0; e < 4; ++e) yb[4 * u + e] = X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u);
     }
   }
-  uint32_t km = 0;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int idx = 4 * ((j >> 2) * NT + tid) + (j & 3);
@@ -458,10 +459,8 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
   const uint32_t ka = block_reduce<uint32_t>(km, OpMax(), sh.redu);  // also orders the bin clearing
   const float A = f32_of_key(ka);
   if (!(ka > KEY_NEG_INF && ka < KEY_POS_INF && fabsf(A) < 1048576.0f)) return false;
-  const float c = A + ANCHOR_UP;
+  c = A + ANCHOR_UP;
 
-  uint32_t nfin = 0;
-  uint32_t bad = 0;  // 1: a value above the bins, 2: NaN
   // branch-free: an element outside the bins adds 0 to the discard slot
   auto add = [&](int idx, float y) __attribute__((always_inline)) {
     const bool valid = idx < V;
@@ -477,7 +476,46 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
   };
 #pragma unroll
   for (int j = 0; j < 16; ++j) add(4 * ((j >> 2) * NT + tid) + (j & 3), yb[j]);
-  row_pass(S, X, [&](int idx, float y, bool) { add(idx, y); }, 4 * NT);
+  const int nch = X.nch;
+  for (int c0 = 4 * NT; c0 < nch; c0 += 4 * NT) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ch = c0 + u * NT + tid;
+      const uint32_t hb = PEN ? X.nibble(ch) : 0u;
+      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) add(4 * ch + e, X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  return true;
+}
+
+// The two-read path.  Returns false, with nothing decided, when the row needs
+// the multi-pass path.  Called by all threads (block-uniform control flow).
+__device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform& X, const RowCfg& R, RowOut& o) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (WAVE - 1);
+  const int V = R.V;
+  o.kmax = 0;
+  o.status = 0;
+  o.tau = KEY_MIN_FINITE;
+  o.CK = static_cast<uint64_t>(KEY_MIN_FINITE) << 32;
+  o.keep_mass = 0;
+  o.keep_n = 0;
+  o.tok = -1;
+
+  // ---------------------------------------------- read 1
+  uint32_t km = 0, nfin = 0, bad = 0;  // bad: 1 a value above the bins, 2 NaN
+  float c = 0.0f;
+  bool anchored;
+  const bool tdiv = X.t > 0.0f;
+  if (X.pen) anchored = tdiv ? read1<true, true>(sh, S, X, V, c, km, nfin, bad) : read1<false, true>(sh, S, X, V, c, km, nfin, bad);
+  else anchored = tdiv ? read1<true, false>(sh, S, X, V, c, km, nfin, bad) : read1<false, false>(sh, S, X, V, c, km, nfin, bad);
+  if (!anchored) return false;
   const uint32_t kmx = block_reduce<uint32_t>(km, OpMax(), sh.redu);
   const uint32_t bad_all = block_reduce<uint32_t>(bad, OpOr(), sh.redu);
   const uint32_t nf = block_reduce<uint32_t>(nfin, OpAdd(), sh.redu);
