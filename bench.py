@@ -77,6 +77,114 @@ def cpu_baseline(w, seconds: float):
                       f"{torch.backends.cpu.get_cpu_capability()}), {dt:.1f} s"}
 
 
+def cpu_baseline_spec(w, seconds: float):
+    """The oracle's speculative verify (per sequence: filtered target and draft
+    softmax at each examined position, accept test, residual or bonus draw) on
+    the first sequences of the workload until ``seconds`` have been spent."""
+    import torch
+
+    from oracle import sampler_oracle as O
+
+    p = O.RowParams(float(w.temperature), 0, float(w.top_p), 0.0, 1.0, [], [])
+    O.speculative_verify(w.target[:1], w.draft[:1], w.draft_ids[:1], p, w.u_accept[:1], w.u_resample[:1])
+    seqs = 0
+    toks = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        b = seqs % w.target.size(0)
+        r = O.speculative_verify(w.target[b:b + 1], w.draft[b:b + 1], w.draft_ids[b:b + 1], p,
+                                 w.u_accept[b:b + 1], w.u_resample[b:b + 1])[0]
+        toks += r.n_accepted + 1
+        seqs += 1
+    dt = time.perf_counter() - t0
+    return {"value": toks / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{seqs} sequences of {w.name} (seed 0, cycling through its {w.target.size(0)}), one oracle "
+                      f"verify per sequence (torch {torch.__version__} CPU, {torch.get_num_threads()} threads), "
+                      f"{dt:.1f} s"}
+
+
+def bench_spec(args, dev) -> int:
+    """Speculative verify: one step = the three launches of one batch (target
+    rows with the bonus draw, draft rows, verify); tokens/s counts accepted
+    drafts plus the resampled or bonus token of every sequence."""
+    import torch
+
+    from rl_project_amd import sample_tokens, workloads
+    from rl_project_amd.speculative import SpecPlan
+
+    def draft_sampler(rows, u):
+        # drafts drawn from the filtered draft distribution by the GPU sampler
+        return sample_tokens(rows.to(dev), temperature=0.8, top_p=0.95, uniforms=u.to(dev)).tokens.cpu()
+
+    ws = [workloads.make_spec(args.workload, seed=0, draft_sampler=draft_sampler)]
+    batch_bytes = (ws[0].target.numel() + ws[0].draft.numel()) * ws[0].target.element_size()
+    nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))
+    for s in range(1, nbuf):
+        ws.append(workloads.make_spec(args.workload, seed=s, draft_sampler=draft_sampler))
+    plans = []
+    for w in ws:
+        wd = w.to(dev)
+        plans.append(SpecPlan(wd.target, wd.draft, wd.draft_ids, temperature=wd.temperature, top_p=wd.top_p,
+                              u_accept=wd.u_accept, u_resample=wd.u_resample, return_ratio=False))
+    stream = torch.cuda.current_stream(dev)
+    for i in range(max(args.warmup, nbuf)):
+        plans[i % nbuf].launch()
+    torch.cuda.synchronize(dev)
+    for pl in plans:
+        if not bool(pl.status_ok().all()):
+            print("speculative rows failed", file=sys.stderr)
+            return 1
+    toks = [int((pl.n_accepted + 1).sum()) for pl in plans]
+
+    K = args.steps
+    timed = list(range(0, K, EV_EVERY))
+    ev_s = {k: torch.cuda.Event(enable_timing=True) for k in timed}
+    ev_e = {k: torch.cuda.Event(enable_timing=True) for k in timed}
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for k in range(K):
+        if k in ev_s:
+            ev_s[k].record(stream)
+            plans[k % nbuf].launch()
+            ev_e[k].record(stream)
+        else:
+            plans[k % nbuf].launch()
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    durs = sorted(ev_s[k].elapsed_time(ev_e[k]) for k in timed)
+    step_ms = sum(durs) / len(durs)
+    w = ws[0]
+    B, Kd = w.draft_ids.shape
+    n_tok = sum(toks[k % nbuf] for k in range(K))
+    alg_bytes = w.algorithmic_bytes()
+    achieved = alg_bytes / (step_ms * 1e-3) / 1e9
+    result = {
+        "metric": f"speculative verify tokens/sec at B={B}, K={Kd}, V={w.target.size(2)} fp32 (accepted + 1 per sequence)",
+        "value": n_tok / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / K,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "sequences": B, "drafts": Kd, "vocab": w.target.size(2),
+                   "input_buffers": nbuf, "tokens_per_step_mean": n_tok / K, "sequences_per_s": B * K / wall},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
+                     "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
+                     "step_ms_p10": durs[len(durs) // 10], "step_ms_p90": durs[(9 * len(durs)) // 10],
+                     "kernel": "k_sample_rows32 (target rows) + k_sample_rows32 (draft rows) + k_spec_verify"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_spec(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +223,8 @@ def main() -> int:
         torch.cuda.synchronize(dev)
         print(json.dumps({"calibrate_copy_bytes": 4 * n, "launches": 5}), flush=True)
         return 0
+    if args.workload.startswith("spec_"):
+        return bench_spec(args, dev)
     w = workloads.make(args.workload, seed=0)
     batch_bytes = w.logits.numel() * w.logits.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))

@@ -15,11 +15,11 @@ SamplingParams
 from .params import GenerationSettings, SamplingParams, SamplingParamsError
 from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, describe_rows, filtered_outputs,
                        generate_tokens, sample_from_logits, sample_tokens)
-from .speculative import SpeculativeGenerator, SpecOutput, speculative_verify
+from .speculative import SpeculativeGenerator, SpecOutput, SpecPlan, speculative_verify
 
 __all__ = [
     "apply_sampling_filters", "sample_from_logits", "generate_tokens",
     "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplingError",
-    "speculative_verify", "SpeculativeGenerator", "SpecOutput",
+    "speculative_verify", "SpeculativeGenerator", "SpecOutput", "SpecPlan",
     "SamplingParams", "GenerationSettings", "SamplingParamsError",
 ]

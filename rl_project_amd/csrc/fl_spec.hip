@@ -89,8 +89,12 @@ __device__ __forceinline__ float prob_of(const fl_row_desc& ds, float y, int64_t
   return kept ? D::rn(expf(y - ds.shift) * ds.inv_mass) : 0.0f;
 }
 
+// Rows up to 262144 elements: at most 64 rounds of NT 16-byte chunks.
+constexpr int MAX_ROUNDS = 64;
+
 struct SharedSpec {
   uint64_t redq[NWAVE];
+  uint64_t seg[MAX_ROUNDS * NWAVE];  // weight sum of each (round, wave) segment
   int32_t n_acc;
   int32_t rejected;
   int32_t token;
@@ -164,57 +168,99 @@ __global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
     const bool aligned = ((reinterpret_cast<uintptr_t>(tp) | reinterpret_cast<uintptr_t>(dp)) & 15u) == 0;
     const int nch = (V + N - 1) / N;
     const int nfull = V / N;
-    const int cpt = (nch + NT - 1) / NT;  // chunks per thread: a contiguous slice
-    const int c0 = min(nch, tid * cpt), c1 = min(nch, c0 + cpt);
+    const int nround = (nch + NT - 1) / NT;
+    const int w = tid / WAVE, lane = tid & (WAVE - 1);
 
-    // f(i, p_i, q_i) over this thread's slice in ascending index order
-    auto slice = [&](auto&& f) __attribute__((always_inline)) {
-      for (int c = c0; c < c1; ++c) {
-        float xt[N], xd[N];
-        if (aligned && c < nfull) {
-          C::unpack(buf_load16(rt, 16u * c, 0u), xt);
-          C::unpack(buf_load16(rd, 16u * c, 0u), xd);
-        } else {
-#pragma unroll
-          for (int e = 0; e < N; ++e) {
-            xt[e] = C::elem(rt, N * c + e);
-            xd[e] = C::elem(rd, N * c + e);
-          }
-        }
+    // f(e, i, p_i, q_i) for the N elements of chunk c (ascending index i = N c + e)
+    auto chunk = [&](int c, auto&& f) __attribute__((always_inline)) {
+      float xt[N], xd[N];
+      if (aligned && c < nfull) {
+        C::unpack(buf_load16(rt, 16u * c, 0u), xt);
+        C::unpack(buf_load16(rd, 16u * c, 0u), xd);
+      } else {
 #pragma unroll
         for (int e = 0; e < N; ++e) {
-          const int i = N * c + e;
-          if (i < V)
-            f(i, prob_of<D>(td, filt_value<D>(xt[e], cap, T), i), prob_of<D>(dd, filt_value<D>(xd[e], cap, T), i));
+          xt[e] = C::elem(rt, N * c + e);
+          xd[e] = C::elem(rd, N * c + e);
         }
+      }
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const int i = N * c + e;
+        if (i < V) f(e, i, prob_of<D>(td, filt_value<D>(xt[e], cap, T), i), prob_of<D>(dd, filt_value<D>(xd[e], cap, T), i));
       }
     };
     auto resid = [](float p, float q) { return fmaxf(D::rn(p - q), 0.0f); };
 
-    // sum(r) in the dtype (:74)
+    // pass 1: sum(r) in the dtype (:74); chunk c of round k is read by thread
+    // c - k * NT, so every wave load covers 64 consecutive chunks
     uint64_t lr = 0;
-    slice([&](int, float p, float q) { lr += fx45(resid(p, q)); });
+    for (int k = 0; k < nround; ++k) chunk(k * NT + tid, [&](int, int, float p, float q) { lr += fx45(resid(p, q)); });
     const uint64_t rsum = block_reduce<uint64_t>(lr, OpAdd(), sh.redq);
     const bool use_p = rsum == 0;  // p == q: the oracle's fallback to p
     const float den = D::rn(D::rn(static_cast<float>(static_cast<double>(rsum) * (1.0 / 35184372088832.0))) + 1e-10f);
     auto weight = [&](float p, float q) { return use_p ? p : D::rn(resid(p, q) / den); };
 
-    uint64_t lw = 0;
-    slice([&](int, float p, float q) { lw += fx45(weight(p, q)); });
-    uint64_t W;
-    const uint64_t base = block_excl_scan<uint64_t>(lw, sh.redq, &W);
-    const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
-    const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(W)));
-    if (lw > 0 && base <= target && target < base + lw) {
-      uint64_t c = base;
-      int found = -1;
-      slice([&](int i, float p, float q) {
-        if (found < 0) {
-          c += fx45(weight(p, q));
-          if (c > target) found = i;
+    // pass 2: weight sums per (round, wave) segment, in ascending index order
+    for (int k = 0; k < nround; ++k) {
+      uint64_t lw = 0;
+      chunk(k * NT + tid, [&](int, int, float p, float q) { lw += fx45(weight(p, q)); });
+      lw = wave_reduce(lw, OpAdd());
+      if (lane == 0) sh.seg[k * NWAVE + w] = lw;
+    }
+    __syncthreads();
+    // wave 0: segment holding the target, then its member by a wave scan
+    if (tid < WAVE) {
+      const int nseg = nround * NWAVE;
+      uint64_t W = 0;
+      for (int j = lane; j < nseg; j += WAVE) W += sh.seg[j];
+      W = wave_reduce(W, OpAdd());
+      const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
+      const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(W)));
+      // first segment whose inclusive sum exceeds target
+      uint64_t base = 0;
+      int seg = -1;
+      for (int j0 = 0; j0 < nseg && seg < 0; j0 += WAVE) {
+        const uint64_t v = j0 + lane < nseg ? sh.seg[j0 + lane] : 0ull;
+        const uint64_t inc = wave_incl_scan(v);
+        const uint64_t m = __ballot(base + inc > target);
+        if (m) {
+          const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+          seg = j0 + f;
+          base += __shfl(inc - v, f, WAVE);
+        } else {
+          base += __shfl(inc, WAVE - 1, WAVE);
         }
-      });
-      sh.token = found;
+      }
+      int found = -1;
+      if (seg >= 0) {
+        // the segment's chunks, one per lane, in ascending order
+        const int c = (seg / NWAVE) * NT + (seg % NWAVE) * WAVE + lane;
+        uint64_t wl[N];
+        uint64_t lc = 0;
+#pragma unroll
+        for (int e = 0; e < N; ++e) wl[e] = 0;
+        if (c < nch) {
+          chunk(c, [&](int e, int, float p, float q) {
+            wl[e] = fx45(weight(p, q));
+            lc += wl[e];
+          });
+        }
+        const uint64_t inc = wave_incl_scan(lc);
+        const uint64_t m = __ballot(base + inc > target);
+        if (m) {
+          const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+          if (lane == f) {
+            uint64_t cc = base + inc - lc;
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+              cc += wl[e];
+              if (found < 0 && cc > target) found = N * c + e;
+            }
+            sh.token = found;
+          }
+        }
+      }
     }
     __syncthreads();
     tok = sh.token < 0 ? V - 1 : sh.token;

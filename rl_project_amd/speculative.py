@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from ._lib import SpecArgs, check, lib, ptr
-from .sampling import _DTYPES, _check_logits, describe_rows, sample_tokens
+from .sampling import FL_FLAG_NO_SELECT, _DTYPES, _Call, _check_logits, sample_tokens
 
 
 @dataclass
@@ -34,6 +34,81 @@ class SpecOutput:
     n_accepted: torch.Tensor        # int32 [B]
     tokens: torch.Tensor            # int64 [B, K+1]: accepted drafts, then the resampled / bonus token, -1 after
     ratio: Optional[torch.Tensor]   # float32 [B, K]: acceptance ratio of each examined draft (NaN if not examined)
+
+
+class SpecPlan:
+    """A prepared ``speculative_verify``: arguments and outputs are built once;
+    each ``launch()`` enqueues the three kernels (target rows with the bonus
+    draw, draft rows, verify) with no allocation and no host synchronisation.
+    The logits, draft ids and uniforms are read at launch time, so a decode
+    loop may overwrite them in place between launches."""
+
+    def __init__(self, target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor, *,
+                 temperature: float = 1.0, top_k: Optional[int] = None, top_p: Optional[float] = None,
+                 min_p: Optional[float] = None, softcap: float = 0.0, u_accept: Optional[torch.Tensor] = None,
+                 u_resample: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
+                 return_ratio: bool = True):
+        if target_logits.dim() != 3 or draft_logits.dim() != 3:
+            raise ValueError("target_logits must be [B, K+1, V] and draft_logits [B, K, V]")
+        B, K1, V = target_logits.shape
+        K = K1 - 1
+        if K < 1 or tuple(draft_logits.shape) != (B, K, V) or tuple(draft_ids.shape) != (B, K):
+            raise ValueError(f"shape mismatch: target {tuple(target_logits.shape)}, draft {tuple(draft_logits.shape)}, "
+                             f"draft_ids {tuple(draft_ids.shape)}")
+        if target_logits.dtype != draft_logits.dtype:
+            raise ValueError("target and draft logits must share a dtype")
+        dev = target_logits.device
+        self.B, self.K = B, K
+        T = max(float(temperature), 1e-8)
+        if u_accept is None:
+            u_accept = torch.rand(B, K, device=dev, generator=generator)
+        if u_resample is None:
+            u_resample = torch.rand(B, device=dev, generator=generator)
+        self.u_accept = u_accept.to(device=dev, dtype=torch.float32).contiguous()
+        self.u_resample = u_resample.to(device=dev, dtype=torch.float32).contiguous()
+        filt = dict(temperature=T, top_k=top_k if (top_k is not None and top_k > 0) else 0,
+                    top_p=top_p if top_p is not None else 1.0, min_p=min_p if min_p is not None else 0.0,
+                    softcap=softcap)
+        tgt = _check_logits(target_logits.reshape(B * K1, V))
+        drf = _check_logits(draft_logits.reshape(B * K, V))
+        self._t = _Call(tgt, flags=0, want_desc=True, uniforms=self.u_resample.repeat_interleave(K1), **filt)
+        self._d = _Call(drf, flags=FL_FLAG_NO_SELECT, want_desc=True, uniforms=None, **filt)
+        self.n_accepted = torch.empty(B, dtype=torch.int32, device=dev)
+        self.tokens = torch.empty(B, K1, dtype=torch.int64, device=dev)
+        self.ratio = torch.empty(B, K, dtype=torch.float32, device=dev) if return_ratio else None
+        self._temps = torch.full((B,), T, dtype=torch.float32, device=dev)
+        self._ids = draft_ids.to(device=dev, dtype=torch.int64).contiguous()
+        a = SpecArgs()
+        a.struct_size = ctypes.sizeof(SpecArgs)
+        a.dtype = _DTYPES[target_logits.dtype]
+        a.target, a.draft = tgt.data_ptr(), drf.data_ptr()
+        a.batch, a.k, a.vocab, a.ld = B, K, V, V
+        a.temperature, a.softcap = self._temps.data_ptr(), float(softcap or 0.0)
+        a.target_desc, a.draft_desc = ptr(self._t.desc), ptr(self._d.desc)
+        a.draft_ids, a.u_accept, a.u_resample = self._ids.data_ptr(), self.u_accept.data_ptr(), self.u_resample.data_ptr()
+        a.bonus_token = self._t.tokens.data_ptr()
+        a.out_n_accepted, a.out_tokens, a.out_ratio = (self.n_accepted.data_ptr(), self.tokens.data_ptr(),
+                                                       ptr(self.ratio))
+        self._args = a
+        self._argp = ctypes.byref(a)
+        self._stream = _lib.stream_handle(dev)
+        self._verify = lib().fl_spec_verify
+
+    def launch(self) -> None:
+        self._t.run()
+        self._d.run()
+        rc = self._verify(self._argp, self._stream)
+        if rc:
+            check(rc, "fl_spec_verify")
+
+    def status_ok(self) -> torch.Tensor:
+        """bool [B]: every target and draft row of the sequence could be sampled."""
+        B, K = self.B, self.K
+        return ~((self._t.status != 0).view(B, K + 1).any(1) | (self._d.status != 0).view(B, K).any(1))
+
+    @property
+    def output(self) -> SpecOutput:
+        return SpecOutput(self.n_accepted, self.tokens, self.ratio)
 
 
 def speculative_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor, *,
@@ -45,55 +120,16 @@ def speculative_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, 
 
     target_logits [B, K+1, V] (positions of the K drafts plus the bonus
     position), draft_logits [B, K, V], draft_ids int64 [B, K]."""
-    if target_logits.dim() != 3 or draft_logits.dim() != 3:
-        raise ValueError("target_logits must be [B, K+1, V] and draft_logits [B, K, V]")
-    B, K1, V = target_logits.shape
-    K = K1 - 1
-    if K < 1 or tuple(draft_logits.shape) != (B, K, V) or tuple(draft_ids.shape) != (B, K):
-        raise ValueError(f"shape mismatch: target {tuple(target_logits.shape)}, draft {tuple(draft_logits.shape)}, "
-                         f"draft_ids {tuple(draft_ids.shape)}")
-    if target_logits.dtype != draft_logits.dtype:
-        raise ValueError("target and draft logits must share a dtype")
-    dev = target_logits.device
-    T = max(float(temperature), 1e-8)
-    if u_accept is None:
-        u_accept = torch.rand(B, K, device=dev, generator=generator)
-    if u_resample is None:
-        u_resample = torch.rand(B, device=dev, generator=generator)
-    u_accept = u_accept.to(device=dev, dtype=torch.float32).contiguous()
-    u_resample = u_resample.to(device=dev, dtype=torch.float32).contiguous()
-    filt = dict(temperature=T, top_k=top_k if (top_k is not None and top_k > 0) else 0,
-                top_p=top_p if top_p is not None else 1.0, min_p=min_p if min_p is not None else 0.0,
-                softcap=softcap)
-    tgt = _check_logits(target_logits.reshape(B * K1, V))
-    drf = _check_logits(draft_logits.reshape(B * K, V))
-    t_out = sample_tokens(tgt, uniforms=u_resample.repeat_interleave(K1), return_desc=True, check_status=False,
-                          **filt)
-    d_desc, d_status = describe_rows(drf, **filt)
-    n_acc = torch.empty(B, dtype=torch.int32, device=dev)
-    tokens = torch.empty(B, K1, dtype=torch.int64, device=dev)
-    ratio = torch.empty(B, K, dtype=torch.float32, device=dev) if return_ratio else None
-    temps = torch.full((B,), T, dtype=torch.float32, device=dev)
-    ids = draft_ids.to(device=dev, dtype=torch.int64).contiguous()
-    a = SpecArgs()
-    a.struct_size = ctypes.sizeof(SpecArgs)
-    a.dtype = _DTYPES[target_logits.dtype]
-    a.target, a.draft = tgt.data_ptr(), drf.data_ptr()
-    a.batch, a.k, a.vocab, a.ld = B, K, V, V
-    a.temperature, a.softcap = temps.data_ptr(), float(softcap or 0.0)
-    a.target_desc, a.draft_desc = ptr(t_out.desc), ptr(d_desc)
-    a.draft_ids, a.u_accept, a.u_resample = ids.data_ptr(), u_accept.data_ptr(), u_resample.data_ptr()
-    a.bonus_token = t_out.tokens.data_ptr()
-    a.out_n_accepted, a.out_tokens, a.out_ratio = n_acc.data_ptr(), tokens.data_ptr(), ptr(ratio)
-    check(lib().fl_spec_verify(ctypes.byref(a), _lib.stream_handle(dev)), "fl_spec_verify")
-    # keep the argument tensors alive until the kernels have consumed them
-    _keep = (tgt, drf, t_out, d_desc, temps, ids, u_accept, u_resample)  # noqa: F841
-    bad = (t_out.status != 0).view(B, K1).any(1) | (d_status != 0).view(B, K).any(1)
-    if bool(bad.any()):
+    plan = SpecPlan(target_logits, draft_logits, draft_ids, temperature=temperature, top_k=top_k, top_p=top_p,
+                    min_p=min_p, softcap=softcap, u_accept=u_accept, u_resample=u_resample, generator=generator,
+                    return_ratio=return_ratio)
+    plan.launch()
+    ok = plan.status_ok()
+    if not bool(ok.all()):
         from .sampling import SamplingError
-        raise SamplingError(f"speculative verify: sequences {torch.nonzero(bad).flatten().tolist()[:8]} have "
+        raise SamplingError(f"speculative verify: sequences {torch.nonzero(~ok).flatten().tolist()[:8]} have "
                             "rows that cannot be sampled (NaN / +inf / fully masked logits)")
-    return SpecOutput(n_acc, tokens, ratio)
+    return plan.output
 
 
 class SpeculativeGenerator:
