@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FL_ABI_VERSION 1
+#define FL_ABI_VERSION 2
 
 enum fl_dtype { FL_DTYPE_F32 = 0, FL_DTYPE_BF16 = 1, FL_DTYPE_F16 = 2 };
 
@@ -185,9 +185,22 @@ typedef struct fl_spec_args {
   int32_t* out_n_accepted;         /* [batch] */
   int64_t* out_tokens;             /* [batch, k+1] */
   float* out_ratio;                /* [batch, k] or NULL */
+  void* workspace;                 /* NULL, or fl_spec_workspace_bytes(batch) bytes of device memory */
+  int64_t workspace_bytes;
 } fl_spec_args;
 
+/*
+ * With a workspace, the residual draw of every rejected sequence is spread
+ * over several work-groups (four launches in stream order); without one, each
+ * sequence runs in a single work-group.  Both give identical results.  The
+ * workspace is scratch owned by the caller: calls that overlap in time must
+ * not share one.
+ */
 int fl_spec_verify(const fl_spec_args* args, void* stream);
+
+/* Bytes of workspace fl_spec_verify uses for `batch` sequences (no counterpart
+ * in the reference, which verifies one sequence at a time). */
+int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes);
 
 /* Thread-local description of the last error returned on this thread. */
 const char* fl_last_error(void);

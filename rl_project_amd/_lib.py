@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflsampler.so")
 
-FL_ABI_VERSION = 1
+FL_ABI_VERSION = 2
 FL_DTYPE_F32, FL_DTYPE_BF16, FL_DTYPE_F16 = 0, 1, 2
 FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
@@ -57,6 +57,7 @@ class SpecArgs(ctypes.Structure):
         ("temperature", _p), ("softcap", ctypes.c_float),
         ("target_desc", _p), ("draft_desc", _p), ("draft_ids", _p), ("u_accept", _p), ("u_resample", _p),
         ("bonus_token", _p), ("out_n_accepted", _p), ("out_tokens", _p), ("out_ratio", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -92,6 +93,8 @@ def lib() -> ctypes.CDLL:
     handle.fl_apply_filter.restype = ctypes.c_int
     handle.fl_spec_verify.argtypes = [ctypes.POINTER(SpecArgs), _p]
     handle.fl_spec_verify.restype = ctypes.c_int
+    handle.fl_spec_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
+    handle.fl_spec_workspace_bytes.restype = ctypes.c_int
     if handle.fl_abi_version() != FL_ABI_VERSION:
         raise SamplerLibraryError(f"ABI version {handle.fl_abi_version()} != {FL_ABI_VERSION}")
     _lib = handle
@@ -113,4 +116,5 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_last_error", "fl_abi_version")
+EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_workspace_bytes", "fl_last_error",
+                    "fl_abi_version")

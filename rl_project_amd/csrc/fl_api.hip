@@ -111,8 +111,22 @@ int fl_spec_verify(const fl_spec_args* a, void* stream) {
   if (!a->temperature || !a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
       !a->u_resample || !a->bonus_token || !a->out_n_accepted || !a->out_tokens)
     return fail(FL_EINVAL, "fl_spec_verify: a required pointer is NULL");
+  if (a->workspace != nullptr && (a->workspace_bytes < 0 ||
+                                  static_cast<size_t>(a->workspace_bytes) < fl::spec_workspace_bytes(a->batch)))
+    return fail(FL_EINVAL, "fl_spec_verify: workspace of %lld bytes, %zu needed", static_cast<long long>(a->workspace_bytes),
+                fl::spec_workspace_bytes(a->batch));
+  if (a->workspace != nullptr && (reinterpret_cast<uintptr_t>(a->workspace) & 7u) != 0)
+    return fail(FL_EINVAL, "fl_spec_verify: workspace not 8-byte aligned");
   const hipError_t e = fl::launch_spec_verify(*a, static_cast<hipStream_t>(stream));
   return check_launch(e, "fl_spec_verify");
+}
+
+int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes) {
+  if (out_bytes == nullptr) return fail(FL_EINVAL, "fl_spec_workspace_bytes: out_bytes is NULL");
+  if (batch < 0 || batch > 0x7fffffff)
+    return fail(FL_EINVAL, "fl_spec_workspace_bytes: bad batch %lld", static_cast<long long>(batch));
+  *out_bytes = fl::spec_workspace_bytes(batch);
+  return ok();
 }
 
 }  // extern "C"

@@ -273,7 +273,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // u outside [0, 1) (or NaN) is clamped into it
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const float CAP = a.softcap;
-  const bool hist_too_long = H_in > FL_MAX_HISTORY;
+  // (H_in is only meaningful with a history: without one it was read from the stand-in array)
+  const bool hist_too_long = a.hist_ids != nullptr && H_in > FL_MAX_HISTORY;
   const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
   const bool sc_entry = SC && (CAP > 0.0f) && !SC_ELEM;

@@ -91,6 +91,10 @@ __device__ __forceinline__ float prob_of(const fl_row_desc& ds, float y, int64_t
 
 // Rows up to 262144 elements: at most 64 rounds of NT 16-byte chunks.
 constexpr int MAX_ROUNDS = 64;
+// Sliced residual: at most this many slices of a row pair per sequence, and
+// this many threads per slice work-group.
+constexpr int MAX_SLICES = 16;
+constexpr int NT_PART = 256;
 
 struct SharedSpec {
   uint64_t redq[NWAVE];
@@ -100,185 +104,349 @@ struct SharedSpec {
   int32_t token;
 };
 
-}  // namespace
-
+// Accept walk of sequence b (one thread): ratio = min(1, p(d)/(q(d)+1e-10))
+// in the logits' dtype (:63), accept iff u_accept < ratio (:65).  Writes the
+// ratios and the accepted drafts; returns the accepted count, *rej = whether
+// a draft was rejected.
 template <class D>
-__global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
-  __shared__ SharedSpec sh;
+__device__ int accept_walk(const fl_spec_args& a, int64_t b, bool* rej) {
   using C = Chunk<D>;
-  constexpr int N = C::N;
-  const int tid = threadIdx.x;
-  const int64_t b = blockIdx.x;
   const int64_t K = a.k;
   const int V = static_cast<int>(a.vocab);
   const float T = a.temperature[b];
-  const float cap = a.softcap;
   const size_t esz = D::id == FL_DTYPE_F32 ? 4 : 2;
-  const char* tgt_base = static_cast<const char*>(a.target);
-  const char* drf_base = static_cast<const char*>(a.draft);
-  auto trow = [&](int64_t i) { return tgt_base + (b * (K + 1) + i) * a.ld * esz; };
-  auto drow = [&](int64_t i) { return drf_base + (b * K + i) * a.ld * esz; };
-
-  // ------------------------------------------------ accept walk (thread 0)
-  if (tid == 0) {
-    int n = 0;
-    bool rej = false;
-    for (int64_t i = 0; i < K; ++i) {
-      const int64_t d = a.draft_ids[b * K + i];
-      float ratio = 0.0f;
-      if (d >= 0 && d < V) {
-        const fl_row_desc td = a.target_desc[b * (K + 1) + i];
-        const fl_row_desc dd = a.draft_desc[b * K + i];
-        const __amdgpu_buffer_rsrc_t rt = row_rsrc(trow(i), static_cast<uint32_t>(V * esz));
-        const __amdgpu_buffer_rsrc_t rd = row_rsrc(drow(i), static_cast<uint32_t>(V * esz));
-        const float p = prob_of<D>(td, filt_value<D>(C::elem(rt, static_cast<int>(d)), cap, T), d);
-        const float q = prob_of<D>(dd, filt_value<D>(C::elem(rd, static_cast<int>(d)), cap, T), d);
-        ratio = fminf(1.0f, D::rn(p / D::rn(q + 1e-10f)));
-      }
-      if (a.out_ratio) a.out_ratio[b * K + i] = ratio;
-      if (a.u_accept[b * K + i] < ratio) {
-        a.out_tokens[b * (K + 1) + i] = d;
-        ++n;
-      } else {
-        rej = true;
-        break;
-      }
+  int n = 0;
+  *rej = false;
+  for (int64_t i = 0; i < K; ++i) {
+    const int64_t d = a.draft_ids[b * K + i];
+    float ratio = 0.0f;
+    if (d >= 0 && d < V) {
+      const fl_row_desc td = a.target_desc[b * (K + 1) + i];
+      const fl_row_desc dd = a.draft_desc[b * K + i];
+      const char* tp = static_cast<const char*>(a.target) + (b * (K + 1) + i) * a.ld * esz;
+      const char* dp = static_cast<const char*>(a.draft) + (b * K + i) * a.ld * esz;
+      const __amdgpu_buffer_rsrc_t rt = row_rsrc(tp, static_cast<uint32_t>(V * esz));
+      const __amdgpu_buffer_rsrc_t rd = row_rsrc(dp, static_cast<uint32_t>(V * esz));
+      const float p = prob_of<D>(td, filt_value<D>(C::elem(rt, static_cast<int>(d)), a.softcap, T), d);
+      const float q = prob_of<D>(dd, filt_value<D>(C::elem(rd, static_cast<int>(d)), a.softcap, T), d);
+      ratio = fminf(1.0f, D::rn(p / D::rn(q + 1e-10f)));
     }
-    if (a.out_ratio)
-      for (int64_t i = n + (rej ? 1 : 0); i < K; ++i) a.out_ratio[b * K + i] = __builtin_nanf("");
-    sh.n_acc = n;
-    sh.rejected = rej ? 1 : 0;
-    sh.token = -1;
+    if (a.out_ratio) a.out_ratio[b * K + i] = ratio;
+    if (a.u_accept[b * K + i] < ratio) {
+      a.out_tokens[b * (K + 1) + i] = d;
+      ++n;
+    } else {
+      *rej = true;
+      break;
+    }
   }
-  __syncthreads();
-  const int n_acc = sh.n_acc;
-  const bool rejected = sh.rejected != 0;
+  if (a.out_ratio)
+    for (int64_t i = n + (*rej ? 1 : 0); i < K; ++i) a.out_ratio[b * K + i] = __builtin_nanf("");
+  return n;
+}
 
-  int64_t tok;
-  if (!rejected) {
-    tok = a.bonus_token[b * (K + 1) + K];
-  } else {
-    // ---------------------------------------------- residual at position n_acc
-    const fl_row_desc td = a.target_desc[b * (K + 1) + n_acc];
-    const fl_row_desc dd = a.draft_desc[b * K + n_acc];
-    const char* tp = trow(n_acc);
-    const char* dp = drow(n_acc);
-    const __amdgpu_buffer_rsrc_t rt = row_rsrc(tp, static_cast<uint32_t>(V * esz));
-    const __amdgpu_buffer_rsrc_t rd = row_rsrc(dp, static_cast<uint32_t>(V * esz));
-    const bool aligned = ((reinterpret_cast<uintptr_t>(tp) | reinterpret_cast<uintptr_t>(dp)) & 15u) == 0;
-    const int nch = (V + N - 1) / N;
-    const int nfull = V / N;
-    const int nround = (nch + NT - 1) / NT;
-    const int w = tid / WAVE, lane = tid & (WAVE - 1);
-
-    // f(e, i, p_i, q_i) for the N elements of chunk c (ascending index i = N c + e)
-    auto chunk = [&](int c, auto&& f) __attribute__((always_inline)) {
-      float xt[N], xd[N];
-      if (aligned && c < nfull) {
-        C::unpack(buf_load16(rt, 16u * c, 0u), xt);
-        C::unpack(buf_load16(rd, 16u * c, 0u), xd);
-      } else {
-#pragma unroll
-        for (int e = 0; e < N; ++e) {
-          xt[e] = C::elem(rt, N * c + e);
-          xd[e] = C::elem(rd, N * c + e);
-        }
-      }
+// The target and draft rows of one position and their filtered probabilities.
+template <class D>
+struct PairRows {
+  using C = Chunk<D>;
+  static constexpr int N = C::N;
+  __amdgpu_buffer_rsrc_t rt, rd;
+  fl_row_desc td, dd;
+  bool aligned;
+  int V, nch, nfull;
+  float cap, T;
+  __device__ PairRows(const fl_spec_args& a, int64_t b, int pos) {
+    const int64_t K = a.k;
+    const size_t esz = D::id == FL_DTYPE_F32 ? 4 : 2;
+    V = static_cast<int>(a.vocab);
+    T = a.temperature[b];
+    cap = a.softcap;
+    td = a.target_desc[b * (K + 1) + pos];
+    dd = a.draft_desc[b * K + pos];
+    const char* tp = static_cast<const char*>(a.target) + (b * (K + 1) + pos) * a.ld * esz;
+    const char* dp = static_cast<const char*>(a.draft) + (b * K + pos) * a.ld * esz;
+    rt = row_rsrc(tp, static_cast<uint32_t>(V * esz));
+    rd = row_rsrc(dp, static_cast<uint32_t>(V * esz));
+    aligned = ((reinterpret_cast<uintptr_t>(tp) | reinterpret_cast<uintptr_t>(dp)) & 15u) == 0;
+    nch = (V + N - 1) / N;
+    nfull = V / N;
+  }
+  // f(e, i, p_i, q_i) for the N elements of chunk c (ascending index i = N c + e)
+  template <class F>
+  __device__ __forceinline__ void chunk(int c, F&& f) const {
+    float xt[N], xd[N];
+    if (aligned && c < nfull) {
+      C::unpack(buf_load16(rt, 16u * c, 0u), xt);
+      C::unpack(buf_load16(rd, 16u * c, 0u), xd);
+    } else {
 #pragma unroll
       for (int e = 0; e < N; ++e) {
-        const int i = N * c + e;
-        if (i < V) f(e, i, prob_of<D>(td, filt_value<D>(xt[e], cap, T), i), prob_of<D>(dd, filt_value<D>(xd[e], cap, T), i));
+        xt[e] = C::elem(rt, N * c + e);
+        xd[e] = C::elem(rd, N * c + e);
       }
-    };
-    auto resid = [](float p, float q) { return fmaxf(D::rn(p - q), 0.0f); };
-
-    // pass 1: sum(r) in the dtype (:74); chunk c of round k is read by thread
-    // c - k * NT, so every wave load covers 64 consecutive chunks
-    uint64_t lr = 0;
-    for (int k = 0; k < nround; ++k) chunk(k * NT + tid, [&](int, int, float p, float q) { lr += fx45(resid(p, q)); });
-    const uint64_t rsum = block_reduce<uint64_t>(lr, OpAdd(), sh.redq);
-    const bool use_p = rsum == 0;  // p == q: the oracle's fallback to p
-    const float den = D::rn(D::rn(static_cast<float>(static_cast<double>(rsum) * (1.0 / 35184372088832.0))) + 1e-10f);
-    auto weight = [&](float p, float q) { return use_p ? p : D::rn(resid(p, q) / den); };
-
-    // pass 2: weight sums per (round, wave) segment, in ascending index order
-    for (int k = 0; k < nround; ++k) {
-      uint64_t lw = 0;
-      chunk(k * NT + tid, [&](int, int, float p, float q) { lw += fx45(weight(p, q)); });
-      lw = wave_reduce(lw, OpAdd());
-      if (lane == 0) sh.seg[k * NWAVE + w] = lw;
     }
-    __syncthreads();
-    // wave 0: segment holding the target, then its member by a wave scan
-    if (tid < WAVE) {
-      const int nseg = nround * NWAVE;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const int i = N * c + e;
+      if (i < V) f(e, i, prob_of<D>(td, filt_value<D>(xt[e], cap, T), i), prob_of<D>(dd, filt_value<D>(xd[e], cap, T), i));
+    }
+  }
+};
+
+template <class D>
+__device__ __forceinline__ float resid_of(float p, float q) { return fmaxf(D::rn(p - q), 0.0f); }
+
+// Residual weights (:73-74): r / (sum(r) + 1e-10) in the dtype, or p where r
+// is all zero (the oracle's fallback).  rsum: sum(r) in 2^-45 fixed point.
+template <class D>
+struct Weight {
+  bool use_p;
+  float den;
+  __device__ explicit Weight(uint64_t rsum) {
+    use_p = rsum == 0;
+    den = D::rn(D::rn(static_cast<float>(static_cast<double>(rsum) * (1.0 / 35184372088832.0))) + 1e-10f);
+  }
+  __device__ __forceinline__ float operator()(float p, float q) const { return use_p ? p : D::rn(resid_of<D>(p, q) / den); }
+};
+
+// Sum over chunks [c0, c1) of fx45(g(p, q)) by the calling thread, chunks
+// interleaved over nthreads threads (coalesced loads).
+template <class D, class G>
+__device__ __forceinline__ uint64_t range_sum(const PairRows<D>& R, int c0, int c1, int nthreads, G&& g) {
+  uint64_t acc = 0;
+  for (int c = c0 + static_cast<int>(threadIdx.x); c < c1; c += nthreads)
+    R.chunk(c, [&](int, int, float p, float q) { acc += fx45(g(p, q)); });
+  return acc;
+}
+
+// Inverse CDF over chunks [c0, c1) with NT threads: the first index whose
+// inclusive weight, added to `base`, exceeds `target`.  With `own_target`
+// the target is floor(u * total) of the range itself and base is 0.  Records
+// each (round, wave) segment's weight sum, then wave 0 finds the segment and
+// scans its 64 chunks.  Returns the index or -1 (to every thread).
+template <class D>
+__device__ int pick_in_range(SharedSpec& sh, const PairRows<D>& R, const Weight<D>& wt, int c0, int c1, bool own_target,
+                             float u, uint64_t base, uint64_t target) {
+  constexpr int N = PairRows<D>::N;
+  const int tid = threadIdx.x;
+  const int w = tid / WAVE, lane = tid & (WAVE - 1);
+  const int nround = (c1 - c0 + NT - 1) / NT;
+  for (int k = 0; k < nround; ++k) {
+    const int c = c0 + k * NT + tid;
+    uint64_t lw = 0;
+    if (c < c1) R.chunk(c, [&](int, int, float p, float q) { lw += fx45(wt(p, q)); });
+    lw = wave_reduce(lw, OpAdd());
+    if (lane == 0) sh.seg[k * NWAVE + w] = lw;
+  }
+  if (tid == 0) sh.token = -1;
+  __syncthreads();
+  if (tid < WAVE) {
+    const int nseg = nround * NWAVE;
+    if (own_target) {
       uint64_t W = 0;
       for (int j = lane; j < nseg; j += WAVE) W += sh.seg[j];
       W = wave_reduce(W, OpAdd());
-      const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
-      const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(W)));
-      // first segment whose inclusive sum exceeds target
-      uint64_t base = 0;
-      int seg = -1;
-      for (int j0 = 0; j0 < nseg && seg < 0; j0 += WAVE) {
-        const uint64_t v = j0 + lane < nseg ? sh.seg[j0 + lane] : 0ull;
-        const uint64_t inc = wave_incl_scan(v);
-        const uint64_t m = __ballot(base + inc > target);
-        if (m) {
-          const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
-          seg = j0 + f;
-          base += __shfl(inc - v, f, WAVE);
-        } else {
-          base += __shfl(inc, WAVE - 1, WAVE);
-        }
+      target = static_cast<uint64_t>(floor(static_cast<double>(u) * static_cast<double>(W)));
+      base = 0;
+    }
+    // first segment whose inclusive sum exceeds target
+    int seg = -1;
+    for (int j0 = 0; j0 < nseg && seg < 0; j0 += WAVE) {
+      const uint64_t v = j0 + lane < nseg ? sh.seg[j0 + lane] : 0ull;
+      const uint64_t inc = wave_incl_scan(v);
+      const uint64_t m = __ballot(base + inc > target);
+      if (m) {
+        const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        seg = j0 + f;
+        base += __shfl(inc - v, f, WAVE);
+      } else {
+        base += __shfl(inc, WAVE - 1, WAVE);
       }
-      int found = -1;
-      if (seg >= 0) {
-        // the segment's chunks, one per lane, in ascending order
-        const int c = (seg / NWAVE) * NT + (seg % NWAVE) * WAVE + lane;
-        uint64_t wl[N];
-        uint64_t lc = 0;
+    }
+    if (seg >= 0) {
+      // the segment's chunks, one per lane, in ascending order
+      const int c = c0 + (seg / NWAVE) * NT + (seg % NWAVE) * WAVE + lane;
+      uint64_t wl[N];
+      uint64_t lc = 0;
 #pragma unroll
-        for (int e = 0; e < N; ++e) wl[e] = 0;
-        if (c < nch) {
-          chunk(c, [&](int e, int, float p, float q) {
-            wl[e] = fx45(weight(p, q));
-            lc += wl[e];
-          });
-        }
-        const uint64_t inc = wave_incl_scan(lc);
-        const uint64_t m = __ballot(base + inc > target);
-        if (m) {
-          const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
-          if (lane == f) {
-            uint64_t cc = base + inc - lc;
+      for (int e = 0; e < N; ++e) wl[e] = 0;
+      if (c < c1) {
+        R.chunk(c, [&](int e, int, float p, float q) {
+          wl[e] = fx45(wt(p, q));
+          lc += wl[e];
+        });
+      }
+      const uint64_t inc = wave_incl_scan(lc);
+      const uint64_t m = __ballot(base + inc > target);
+      if (m) {
+        const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        if (lane == f) {
+          uint64_t cc = base + inc - lc;
+          int found = -1;
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-              cc += wl[e];
-              if (found < 0 && cc > target) found = N * c + e;
-            }
-            sh.token = found;
+          for (int e = 0; e < N; ++e) {
+            cc += wl[e];
+            if (found < 0 && cc > target) found = N * c + e;
           }
+          sh.token = found;
         }
       }
     }
-    __syncthreads();
-    tok = sh.token < 0 ? V - 1 : sh.token;
   }
-
-  // ------------------------------------------------ outputs
-  if (tid == 0) {
-    a.out_n_accepted[b] = n_acc;
-    a.out_tokens[b * (K + 1) + n_acc] = tok;
-    for (int64_t i = n_acc + 1; i <= K; ++i) a.out_tokens[b * (K + 1) + i] = -1;
-  }
+  __syncthreads();
+  return sh.token;
 }
 
+__device__ __forceinline__ void write_tail(const fl_spec_args& a, int64_t b, int n_acc, int64_t tok) {
+  const int64_t K = a.k;
+  a.out_n_accepted[b] = n_acc;
+  a.out_tokens[b * (K + 1) + n_acc] = tok;
+  for (int64_t i = n_acc + 1; i <= K; ++i) a.out_tokens[b * (K + 1) + i] = -1;
+}
+
+// Slices of a row pair for the sliced residual path.
+__host__ __device__ inline int spec_slices(int64_t batch) {
+  int64_t s = batch > 0 ? 512 / batch : 1;
+  return static_cast<int>(s < 1 ? 1 : (s > MAX_SLICES ? MAX_SLICES : s));
+}
+
+// Workspace of the sliced path: int32 state[batch] (rejected position or -1),
+// padded to 8 bytes, then uint64 part1[batch * S] and part2[batch * S].
+struct SpecWs {
+  int32_t* state;
+  uint64_t* part1;
+  uint64_t* part2;
+  int S;
+};
+__host__ __device__ inline size_t spec_ws_bytes(int64_t batch) {
+  const int S = spec_slices(batch);
+  return ((static_cast<size_t>(batch) * 4 + 7) & ~static_cast<size_t>(7)) + 16u * static_cast<size_t>(batch) * S;
+}
+__host__ __device__ inline SpecWs spec_ws(void* p, int64_t batch) {
+  SpecWs w;
+  w.S = spec_slices(batch);
+  w.state = static_cast<int32_t*>(p);
+  char* q = static_cast<char*>(p) + ((static_cast<size_t>(batch) * 4 + 7) & ~static_cast<size_t>(7));
+  w.part1 = reinterpret_cast<uint64_t*>(q);
+  w.part2 = w.part1 + batch * w.S;
+  return w;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- one work-group per sequence
+template <class D>
+__global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
+  __shared__ SharedSpec sh;
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  if (tid == 0) {
+    bool rej;
+    sh.n_acc = accept_walk<D>(a, b, &rej);
+    sh.rejected = rej ? 1 : 0;
+  }
+  __syncthreads();
+  const int n_acc = sh.n_acc;
+  int64_t tok;
+  if (!sh.rejected) {
+    tok = a.bonus_token[b * (a.k + 1) + a.k];
+  } else {
+    // residual at position n_acc: pass 1 sums r, pass 2 draws
+    const PairRows<D> R(a, b, n_acc);
+    const uint64_t lr = range_sum(R, 0, R.nch, NT, [](float p, float q) { return resid_of<D>(p, q); });
+    const uint64_t rsum = block_reduce<uint64_t>(lr, OpAdd(), sh.redq);
+    const Weight<D> wt(rsum);
+    const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
+    const int t = pick_in_range(sh, R, wt, 0, R.nch, true, U, 0, 0);
+    tok = t < 0 ? R.V - 1 : t;
+  }
+  if (tid == 0) write_tail(a, b, n_acc, tok);
+}
+
+// ---------------------------------------------------------------- sliced path
+// 1. accept walk per sequence; a sequence with no rejection is finished here
+template <class D>
+__global__ __launch_bounds__(WAVE) void k_spec_accept(const fl_spec_args a, SpecWs ws) {
+  const int64_t b = blockIdx.x;
+  if (threadIdx.x != 0) return;
+  bool rej;
+  const int n = accept_walk<D>(a, b, &rej);
+  ws.state[b] = rej ? n : -1;
+  if (rej) a.out_n_accepted[b] = n;
+  else write_tail(a, b, n, a.bonus_token[b * (a.k + 1) + a.k]);
+}
+
+// 2. per slice of the rejected position's row pair: sum(r) (PASS2 false), or
+//    the sum of the weights (PASS2 true, after every slice's sum(r))
+template <class D, bool PASS2>
+__global__ __launch_bounds__(NT_PART) void k_spec_part(const fl_spec_args a, SpecWs ws) {
+  __shared__ uint64_t red[NT_PART / WAVE];
+  const int64_t b = blockIdx.y;
+  const int s = blockIdx.x;
+  const int pos = ws.state[b];
+  if (pos < 0) return;
+  const PairRows<D> R(a, b, pos);
+  const int cps = (R.nch + ws.S - 1) / ws.S;
+  const int c0 = min(R.nch, s * cps), c1 = min(R.nch, c0 + cps);
+  uint64_t v;
+  if constexpr (!PASS2) {
+    v = range_sum(R, c0, c1, NT_PART, [](float p, float q) { return resid_of<D>(p, q); });
+  } else {
+    uint64_t rsum = 0;
+    for (int j = 0; j < ws.S; ++j) rsum += ws.part1[b * ws.S + j];
+    const Weight<D> wt(rsum);
+    v = range_sum(R, c0, c1, NT_PART, wt);
+  }
+  v = block_reduce<uint64_t, OpAdd, NT_PART / WAVE>(v, OpAdd(), red);
+  if (threadIdx.x == 0) (PASS2 ? ws.part2 : ws.part1)[b * ws.S + s] = v;
+}
+
+// 3. the slice holding floor(u * W), then the member inside it
+template <class D>
+__global__ __launch_bounds__(NT) void k_spec_pick(const fl_spec_args a, SpecWs ws) {
+  __shared__ SharedSpec sh;
+  const int64_t b = blockIdx.x;
+  const int pos = ws.state[b];
+  if (pos < 0) return;
+  const PairRows<D> R(a, b, pos);
+  uint64_t rsum = 0, W = 0;
+  for (int j = 0; j < ws.S; ++j) {
+    rsum += ws.part1[b * ws.S + j];
+    W += ws.part2[b * ws.S + j];
+  }
+  const Weight<D> wt(rsum);
+  const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
+  const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(W)));
+  int s = 0;
+  uint64_t base = 0;
+  while (s < ws.S - 1 && base + ws.part2[b * ws.S + s] <= target) base += ws.part2[b * ws.S + s++];
+  const int cps = (R.nch + ws.S - 1) / ws.S;
+  const int c0 = min(R.nch, s * cps), c1 = min(R.nch, c0 + cps);
+  const int t = pick_in_range(sh, R, wt, c0, c1, false, U, base, target);
+  if (threadIdx.x == 0) write_tail(a, b, pos, t < 0 ? R.V - 1 : t);
+}
+
+size_t spec_workspace_bytes(int64_t batch) { return spec_ws_bytes(batch); }
+
 hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(a.batch)), block(NT);
-  if (a.dtype == FL_DTYPE_F32) hipLaunchKernelGGL(k_spec_verify<F32>, grid, block, 0, s, a);
-  else if (a.dtype == FL_DTYPE_BF16) hipLaunchKernelGGL(k_spec_verify<BF16>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(k_spec_verify<F16>, grid, block, 0, s, a);
+  const bool sliced = a.workspace != nullptr;
+  const SpecWs ws = sliced ? spec_ws(a.workspace, a.batch) : SpecWs{};
+  const dim3 grid(static_cast<unsigned>(a.batch));
+  auto run = [&](auto tag) {
+    using D = decltype(tag);
+    if (!sliced) {
+      hipLaunchKernelGGL(k_spec_verify<D>, grid, dim3(NT), 0, s, a);
+      return;
+    }
+    const dim3 pgrid(static_cast<unsigned>(ws.S), static_cast<unsigned>(a.batch));
+    hipLaunchKernelGGL(k_spec_accept<D>, grid, dim3(WAVE), 0, s, a, ws);
+    hipLaunchKernelGGL((k_spec_part<D, false>), pgrid, dim3(NT_PART), 0, s, a, ws);
+    hipLaunchKernelGGL((k_spec_part<D, true>), pgrid, dim3(NT_PART), 0, s, a, ws);
+    hipLaunchKernelGGL(k_spec_pick<D>, grid, dim3(NT), 0, s, a, ws);
+  };
+  if (a.dtype == FL_DTYPE_F32) run(F32{});
+  else if (a.dtype == FL_DTYPE_BF16) run(BF16{});
+  else run(F16{});
   return hipGetLastError();
 }
 

@@ -41,13 +41,16 @@ class SpecPlan:
     each ``launch()`` enqueues the three kernels (target rows with the bonus
     draw, draft rows, verify) with no allocation and no host synchronisation.
     The logits, draft ids and uniforms are read at launch time, so a decode
-    loop may overwrite them in place between launches."""
+    loop may overwrite them in place between launches.  ``sliced`` spreads the
+    residual draw of each rejected sequence over several work-groups (with a
+    workspace allocated here); ``sliced=False`` runs one work-group per
+    sequence.  Both give identical results."""
 
     def __init__(self, target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor, *,
                  temperature: float = 1.0, top_k: Optional[int] = None, top_p: Optional[float] = None,
                  min_p: Optional[float] = None, softcap: float = 0.0, u_accept: Optional[torch.Tensor] = None,
                  u_resample: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
-                 return_ratio: bool = True):
+                 return_ratio: bool = True, sliced: bool = True):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
             raise ValueError("target_logits must be [B, K+1, V] and draft_logits [B, K, V]")
         B, K1, V = target_logits.shape
@@ -89,6 +92,12 @@ class SpecPlan:
         a.bonus_token = self._t.tokens.data_ptr()
         a.out_n_accepted, a.out_tokens, a.out_ratio = (self.n_accepted.data_ptr(), self.tokens.data_ptr(),
                                                        ptr(self.ratio))
+        # scratch of the sliced residual draw (several work-groups per sequence)
+        nbytes = ctypes.c_size_t(0)
+        check(lib().fl_spec_workspace_bytes(B, ctypes.byref(nbytes)), "fl_spec_workspace_bytes")
+        self._ws = torch.empty(max(int(nbytes.value), 8), dtype=torch.uint8, device=dev) if sliced else None
+        a.workspace = ptr(self._ws)
+        a.workspace_bytes = int(nbytes.value) if sliced else 0
         self._args = a
         self._argp = ctypes.byref(a)
         self._stream = _lib.stream_handle(dev)

@@ -144,3 +144,24 @@ def test_spec_argument_errors():
     assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_ENOTSUP
     s.struct_size = 4
     assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL
+
+
+def test_spec_workspace_bytes_and_checks():
+    L = _lib.lib()
+    n = ctypes.c_size_t(0)
+    assert L.fl_spec_workspace_bytes(32, ctypes.byref(n)) == _lib.FL_OK
+    # int32 state per sequence (padded to 8 bytes), two uint64 slice sums per slice (16 slices at 32 sequences)
+    assert n.value == 128 + 2 * 8 * 32 * 16
+    assert L.fl_spec_workspace_bytes(-1, ctypes.byref(n)) == _lib.FL_EINVAL
+    assert L.fl_spec_workspace_bytes(4, None) == _lib.FL_EINVAL
+    s = _lib.SpecArgs()
+    s.struct_size = ctypes.sizeof(_lib.SpecArgs)
+    s.dtype, s.batch, s.k, s.vocab, s.ld = 0, 2, 2, 16, 16
+    for f in ("temperature", "target", "draft", "target_desc", "draft_desc", "draft_ids", "u_accept", "u_resample",
+              "bonus_token", "out_n_accepted", "out_tokens"):
+        setattr(s, f, 0x1000)
+    s.workspace, s.workspace_bytes = 0x2000, 8          # too small: rejected before any launch
+    assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL
+    assert "workspace" in L.fl_last_error().decode()
+    s.workspace, s.workspace_bytes = 0x2004, 1 << 20    # misaligned
+    assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL

@@ -98,3 +98,23 @@ def test_hetero_bf16_full_vocab():
     print(summ)
     bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
     assert not bad, bad[:4]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_no_history_scalar_params(dtype):
+    """No history ids at all (hist_ids NULL) and scalar parameters: the plain
+    call of the reference's sampler on a 16-bit batch."""
+    import dataclasses
+    B, V = 12, 50000
+    print(f"[no history {dtype}] B={B} V={V}", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=11, batch=B, vocab=V)
+    g = torch.Generator().manual_seed(11)
+    w = dataclasses.replace(w, logits=(2.0 * torch.randn(B, V, generator=g)).to(dtype), history=None,
+                            temperature=torch.full((B,), 0.8), top_k=torch.zeros(B, dtype=torch.int32),
+                            top_p=torch.full((B,), 0.95), min_p=torch.zeros(B), repetition_penalty=torch.ones(B))
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0, status.tolist()
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
