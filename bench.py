@@ -11,8 +11,9 @@ are rotated so that the 256 MB Infinity Cache cannot serve a repeated batch.
 
 Prints one JSON line: rows/s (= sampled tokens/s) over exactly K timed steps
 bracketed by device synchronisations, the dominant kernel's roofline (its
-average launch duration from HIP events on the launch stream, against the
-algorithmic bytes of one launch and MI355X's 8 TB/s HBM peak), and the CPU
+average launch duration from a HIP event pair on the launch stream around the
+K back-to-back launches, against the algorithmic bytes of one launch and
+MI355X's 8 TB/s HBM peak), and the CPU
 baseline (the oracle's per-row restatement of the reference sampler, timed on
 this host on a bounded sample of the same workload).
 """
@@ -26,8 +27,8 @@ import os
 import sys
 import time
 
-EV_EVERY = 10  # launches per timed event pair
 HBM_PEAK_GBS = 8000.0
+ISOLATED = 20  # launches timed one by one for the spread
 METRIC = "sampled rows/sec at B=256,V=128256 mixed params; achieved HBM GB/s vs peak"
 DEFAULT_WORKLOAD = "hetero_bf16_256x128256"
 MALL_BYTES = 256 * 1024 * 1024
@@ -43,6 +44,35 @@ def _traffic_from_profile(workload: str):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def _timed_region(torch, dev, stream, K: int, launch):
+    """K back-to-back launches bracketed by synchronisations (wall clock) and
+    by one HIP event pair on the launch stream.  Returns (mean ms per launch
+    from the events, wall seconds)."""
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for k in range(K):
+        launch(k)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / K, wall
+
+
+def _isolated_launches(torch, dev, stream, launch, n: int = ISOLATED):
+    """Durations (ms, sorted) of n launches each bracketed by its own event
+    pair, outside the timed region: the spread of a single launch (each pair
+    adds a few microseconds of its own)."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for k, (a, b) in enumerate(ev):
+        a.record(stream)
+        launch(k)
+        b.record(stream)
+    torch.cuda.synchronize(dev)
+    return sorted(a.elapsed_time(b) for a, b in ev)
 
 
 def cpu_baseline(w, seconds: float):
@@ -137,22 +167,8 @@ def bench_spec(args, dev) -> int:
     toks = [int((pl.n_accepted + 1).sum()) for pl in plans]
 
     K = args.steps
-    timed = list(range(0, K, EV_EVERY))
-    ev_s = {k: torch.cuda.Event(enable_timing=True) for k in timed}
-    ev_e = {k: torch.cuda.Event(enable_timing=True) for k in timed}
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for k in range(K):
-        if k in ev_s:
-            ev_s[k].record(stream)
-            plans[k % nbuf].launch()
-            ev_e[k].record(stream)
-        else:
-            plans[k % nbuf].launch()
-    torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
-    durs = sorted(ev_s[k].elapsed_time(ev_e[k]) for k in timed)
-    step_ms = sum(durs) / len(durs)
+    step_ms, wall = _timed_region(torch, dev, stream, K, lambda k: plans[k % nbuf].launch())
+    durs = _isolated_launches(torch, dev, stream, lambda k: plans[k % nbuf].launch())
     w = ws[0]
     B, Kd = w.draft_ids.shape
     n_tok = sum(toks[k % nbuf] for k in range(K))
@@ -176,7 +192,8 @@ def bench_spec(args, dev) -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
                      "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
-                     "step_ms_p10": durs[len(durs) // 10], "step_ms_p90": durs[(9 * len(durs)) // 10],
+                     "isolated_step_ms_p10": durs[len(durs) // 10],
+                     "isolated_step_ms_p90": durs[(9 * len(durs)) // 10],
                      "kernel": "k_sample_rows32 (target rows) + k_sample_rows32 (draft rows) + k_spec_verify"},
     }
     if not args.no_cpu_baseline:
@@ -244,26 +261,9 @@ def main() -> int:
         print(f"rows failed: status {status.tolist()[:16]}", file=sys.stderr)
         return 1
 
-    # Kernel durations come from HIP event pairs on the launch stream around
-    # every EV_EVERY-th launch of the timed region: an event pair around each
-    # launch would add its own gap to every step.
     K = args.steps
-    timed = list(range(0, K, EV_EVERY))
-    ev_s = {k: torch.cuda.Event(enable_timing=True) for k in timed}
-    ev_e = {k: torch.cuda.Event(enable_timing=True) for k in timed}
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for k in range(K):
-        if k in ev_s:
-            ev_s[k].record(stream)
-            plans[k % nbuf].launch()
-            ev_e[k].record(stream)
-        else:
-            plans[k % nbuf].launch()
-    torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
-    durs = sorted(ev_s[k].elapsed_time(ev_e[k]) for k in timed)
-    kern_ms = sum(durs) / len(durs)
+    kern_ms, wall = _timed_region(torch, dev, stream, K, lambda k: plans[k % nbuf].launch())
+    durs = _isolated_launches(torch, dev, stream, lambda k: plans[k % nbuf].launch())
 
     B = w.batch
     alg_bytes = w.algorithmic_bytes()
@@ -288,7 +288,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
                      "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
-                     "kernel_ms_p10": durs[len(durs) // 10], "kernel_ms_p90": durs[(9 * len(durs)) // 10],
+                     "isolated_launch_ms_p10": durs[len(durs) // 10],
+                     "isolated_launch_ms_p90": durs[(9 * len(durs)) // 10],
                      "kernel": "k_sample_rows16<BF16, false>" if w.logits.element_size() == 2 else "k_sample_rows32"},
     }
     if not args.no_cpu_baseline:
