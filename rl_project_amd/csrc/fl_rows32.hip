@@ -295,6 +295,30 @@ __device__ void bitonic_desc(uint64_t* buf, int n) {
   }
 }
 
+// Descending order of buf[0, n), n <= NT, whose nonzero entries are distinct
+// (zeros sort last): each thread's entry goes to its rank, the number of
+// entries greater than it, counted over broadcast LDS reads -- independent
+// loads, where a bitonic network for a few hundred entries is a chain of
+// dependent LDS round trips.  tmp: scratch of n entries.  Entries of rank
+// >= the nonzero count are left unspecified.
+__device__ void rank_sort_desc(uint64_t* buf, uint64_t* tmp, int n) {
+  const int t = threadIdx.x;
+  const uint64_t mine = t < n ? buf[t] : 0ull;
+  int r = 0;
+  if ((t & ~(WAVE - 1)) < n) {  // waves holding an entry
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      const uint64_t a0 = buf[j], a1 = buf[j + 1], a2 = buf[j + 2], a3 = buf[j + 3];
+      r += (a0 > mine ? 1 : 0) + (a1 > mine ? 1 : 0) + (a2 > mine ? 1 : 0) + (a3 > mine ? 1 : 0);
+    }
+    for (; j < n; ++j) r += buf[j] > mine ? 1 : 0;
+  }
+  if (t < n && mine != 0ull) tmp[r] = mine;
+  __syncthreads();
+  if (t < n) buf[t] = tmp[t];
+  __syncthreads();
+}
+
 enum Crit { CRIT_COUNT = 0, CRIT_PRED = 1, CRIT_MASS = 2 };
 
 // The bin holding a decision point, scanning bins in descending key order
@@ -798,7 +822,9 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     }
     nm = block_reduce<uint32_t>(nm, OpAdd(), sh.redu);
     if (nm != static_cast<uint32_t>(ngath)) return false;
-    bitonic_desc(sh.cand, ns);  // members first (every member word is nonzero)
+    // members first (every member word is nonzero)
+    if (ns <= NT) rank_sort_desc(sh.cand, sh.cscan, ns);
+    else bitonic_desc(sh.cand, ns);
     const int n = ngath;
 
     // inclusive mass prefix at each candidate
