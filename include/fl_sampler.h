@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FL_ABI_VERSION 2
+#define FL_ABI_VERSION 3
 
 enum fl_dtype { FL_DTYPE_F32 = 0, FL_DTYPE_BF16 = 1, FL_DTYPE_F16 = 2 };
 
@@ -201,6 +201,41 @@ int fl_spec_verify(const fl_spec_args* args, void* stream);
 /* Bytes of workspace fl_spec_verify uses for `batch` sequences (no counterpart
  * in the reference, which verifies one sequence at a time). */
 int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes);
+
+/*
+ * Full-distribution statistics of `rows` logits rows in one pass, in float32
+ * as the reference computes them after .float():
+ *   out_logprob[r] = -cross_entropy(x_r, labels[r])   (models/policy.py:47-50;
+ *                    -0.0 where labels[r] == ignore_index, NaN if out of range)
+ *   out_entropy[r] = -(softmax(x_r) * log_softmax(x_r)).sum()
+ *                                                      (training/common/logprobs.py:65-68)
+ *   out_kl[r]      = (softmax(x_r) * (log_softmax(x_r) - log_softmax(y_r))).sum()
+ *                    with y = ref_logits               (training/common/logprobs.py:58-62)
+ *   out_lse[r]     = log(sum(exp(x_r)))
+ * Row r of logits starts at logits + r * ld elements (ref_logits: r * ref_ld).
+ * ref_logits (same dtype) is required for out_kl; labels for out_logprob.
+ * Every output may be NULL.
+ */
+typedef struct fl_row_stats_args {
+  uint32_t struct_size;
+  int32_t dtype;
+  const void* logits;
+  const void* ref_logits;
+  int64_t rows;
+  int64_t vocab;
+  int64_t ld;
+  int64_t ref_ld;
+  const int64_t* labels;
+  int64_t ignore_index;
+  float* out_logprob;
+  float* out_entropy;
+  float* out_kl;
+  float* out_lse;
+} fl_row_stats_args;
+
+#define FL_MAX_VOCAB_STATS (1 << 24)  /* elements per row for fl_row_stats */
+
+int fl_row_stats(const fl_row_stats_args* args, void* stream);
 
 /* Thread-local description of the last error returned on this thread. */
 const char* fl_last_error(void);

@@ -8,6 +8,9 @@ sample_tokens, describe_rows, filtered_outputs
     Batched entry points with heterogeneous per-row parameters.
 speculative_verify, SpeculativeGenerator
     Speculative-decoding accept / resample (models/generation/speculative.py).
+token_logprobs_from_logits, entropy_from_logits, kl_full_distribution, row_stats
+    Full-distribution log-prob / entropy / KL in one pass (models/policy.py,
+    training/common/logprobs.py).
 SamplingParams
     Per-request parameters with the reference's validation (inference/requests.py).
 """
@@ -16,10 +19,12 @@ from .params import GenerationSettings, SamplingParams, SamplingParamsError
 from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, describe_rows, filtered_outputs,
                        generate_tokens, sample_from_logits, sample_tokens)
 from .speculative import SpeculativeGenerator, SpecOutput, SpecPlan, speculative_verify
+from .logprobs import RowStats, entropy_from_logits, kl_full_distribution, row_stats, token_logprobs_from_logits
 
 __all__ = [
     "apply_sampling_filters", "sample_from_logits", "generate_tokens",
     "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplingError",
     "speculative_verify", "SpeculativeGenerator", "SpecOutput", "SpecPlan",
+    "row_stats", "RowStats", "token_logprobs_from_logits", "entropy_from_logits", "kl_full_distribution",
     "SamplingParams", "GenerationSettings", "SamplingParamsError",
 ]

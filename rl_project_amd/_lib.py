@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflsampler.so")
 
-FL_ABI_VERSION = 2
+FL_ABI_VERSION = 3
 FL_DTYPE_F32, FL_DTYPE_BF16, FL_DTYPE_F16 = 0, 1, 2
 FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
@@ -61,6 +61,16 @@ class SpecArgs(ctypes.Structure):
     ]
 
 
+class RowStatsArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32), ("dtype", ctypes.c_int32),
+        ("logits", _p), ("ref_logits", _p),
+        ("rows", ctypes.c_int64), ("vocab", ctypes.c_int64), ("ld", ctypes.c_int64), ("ref_ld", ctypes.c_int64),
+        ("labels", _p), ("ignore_index", ctypes.c_int64),
+        ("out_logprob", _p), ("out_entropy", _p), ("out_kl", _p), ("out_lse", _p),
+    ]
+
+
 # fl_row_desc: {float y_cut; int32 idx_cut; float shift; float inv_mass; double mass; int32 status; int32 n_kept}
 ROW_DESC_BYTES = 32
 
@@ -95,6 +105,8 @@ def lib() -> ctypes.CDLL:
     handle.fl_spec_verify.restype = ctypes.c_int
     handle.fl_spec_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
     handle.fl_spec_workspace_bytes.restype = ctypes.c_int
+    handle.fl_row_stats.argtypes = [ctypes.POINTER(RowStatsArgs), _p]
+    handle.fl_row_stats.restype = ctypes.c_int
     if handle.fl_abi_version() != FL_ABI_VERSION:
         raise SamplerLibraryError(f"ABI version {handle.fl_abi_version()} != {FL_ABI_VERSION}")
     _lib = handle
@@ -116,5 +128,5 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_workspace_bytes", "fl_last_error",
-                    "fl_abi_version")
+EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_workspace_bytes", "fl_row_stats",
+                    "fl_last_error", "fl_abi_version")

@@ -121,6 +121,26 @@ int fl_spec_verify(const fl_spec_args* a, void* stream) {
   return check_launch(e, "fl_spec_verify");
 }
 
+int fl_row_stats(const fl_row_stats_args* a, void* stream) {
+  if (a == nullptr) return fail(FL_EINVAL, "fl_row_stats: args is NULL");
+  if (a->struct_size != sizeof(fl_row_stats_args)) return fail(FL_EINVAL, "fl_row_stats: struct_size mismatch");
+  if (a->dtype != FL_DTYPE_F32 && a->dtype != FL_DTYPE_BF16 && a->dtype != FL_DTYPE_F16)
+    return fail(FL_EINVAL, "fl_row_stats: unknown dtype %d", a->dtype);
+  if (a->rows < 0 || a->vocab < 1 || a->ld < a->vocab || (a->ref_logits && a->ref_ld < a->vocab))
+    return fail(FL_EINVAL, "fl_row_stats: bad shape rows=%lld vocab=%lld ld=%lld ref_ld=%lld",
+                static_cast<long long>(a->rows), static_cast<long long>(a->vocab), static_cast<long long>(a->ld),
+                static_cast<long long>(a->ref_ld));
+  if (a->vocab > FL_MAX_VOCAB_STATS || a->rows > 0x7fffffff)
+    return fail(FL_ENOTSUP, "fl_row_stats: vocab %lld or rows %lld beyond this build's limits",
+                static_cast<long long>(a->vocab), static_cast<long long>(a->rows));
+  if (a->out_kl && !a->ref_logits) return fail(FL_EINVAL, "fl_row_stats: out_kl needs ref_logits");
+  if (a->out_logprob && !a->labels) return fail(FL_EINVAL, "fl_row_stats: out_logprob needs labels");
+  if (a->rows == 0) return ok();
+  if (!a->logits) return fail(FL_EINVAL, "fl_row_stats: logits is NULL");
+  const hipError_t e = fl::launch_row_stats(*a, static_cast<hipStream_t>(stream));
+  return check_launch(e, "fl_row_stats");
+}
+
 int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes) {
   if (out_bytes == nullptr) return fail(FL_EINVAL, "fl_spec_workspace_bytes: out_bytes is NULL");
   if (batch < 0 || batch > 0x7fffffff)

@@ -314,3 +314,71 @@ def test_spec_emits_target_distribution():
     expected = pt.numpy() * n
     chi2 = float(((counts - expected) ** 2 / expected).sum())
     assert chi2 < 24.3   # chi-square(7 dof) 0.999 quantile
+
+
+# ---------------------------------------------------------------------------
+# Full-distribution statistics (oracle/logprob_oracle.py)
+# ---------------------------------------------------------------------------
+
+def test_rowstats_oracle_uniform_rows():
+    """Uniform logits: entropy log V, every label log-prob -log V, KL to itself
+    0, log-sum-exp c + log V."""
+    import math
+
+    from oracle import logprob_oracle as L
+    V = 1000
+    x = torch.full((2, 3, V), 4.25)
+    lab = torch.tensor([[0, 5, 999], [17, 2, 500]])
+    assert torch.allclose(L.entropy_from_logits(x), torch.full((2, 3), math.log(V)), atol=1e-5)
+    assert torch.allclose(L.token_logprobs_from_logits(x, lab), torch.full((2, 3), -math.log(V)), atol=1e-5)
+    assert torch.allclose(L.kl_full_distribution(x, x), torch.zeros(2, 3), atol=1e-6)
+    assert torch.allclose(L.logsumexp(x), torch.full((2, 3), 4.25 + math.log(V)), atol=1e-5)
+
+
+def test_rowstats_oracle_two_point_closed_form():
+    """V = 2: p = sigmoid(a - b); entropy -p ln p - q ln q; KL(p || r) by hand."""
+    import math
+
+    from oracle import logprob_oracle as L
+    a, b, c, d = 1.3, -0.4, 0.2, 0.9
+    p = 1.0 / (1.0 + math.exp(-(a - b)))
+    r = 1.0 / (1.0 + math.exp(-(c - d)))
+    H = -p * math.log(p) - (1 - p) * math.log(1 - p)
+    KL = p * math.log(p / r) + (1 - p) * math.log((1 - p) / (1 - r))
+    x = torch.tensor([[a, b]])
+    y = torch.tensor([[c, d]])
+    assert abs(float(L.entropy_from_logits(x)[0]) - H) < 1e-6
+    assert abs(float(L.kl_full_distribution(x, y)[0]) - KL) < 1e-6
+    assert abs(float(L.token_logprobs_from_logits(x, torch.tensor([1]))[0]) - math.log(1 - p)) < 1e-6
+
+
+def test_rowstats_oracle_float64_brute_force_and_shift():
+    """Random rows against explicit float64 formulas; adding a constant to a
+    row changes none of the statistics."""
+    from oracle import logprob_oracle as L
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 777, generator=g) * 3.0
+    y = torch.randn(4, 777, generator=g) * 2.0
+    lab = torch.randint(0, 777, (4,), generator=g)
+    xd, yd = x.double(), y.double()
+    lpx = xd - torch.logsumexp(xd, -1, keepdim=True)
+    lpy = yd - torch.logsumexp(yd, -1, keepdim=True)
+    H = -(lpx.exp() * lpx).sum(-1)
+    KL = (lpx.exp() * (lpx - lpy)).sum(-1)
+    LP = lpx.gather(1, lab[:, None])[:, 0]
+    assert torch.allclose(L.entropy_from_logits(x).double(), H, atol=2e-5)
+    assert torch.allclose(L.kl_full_distribution(x, y).double(), KL, atol=2e-5)
+    assert torch.allclose(L.token_logprobs_from_logits(x, lab).double(), LP, atol=2e-5)
+    assert torch.allclose(L.entropy_from_logits(x + 11.0), L.entropy_from_logits(x), atol=2e-5)
+    assert torch.allclose(L.kl_full_distribution(x - 3.0, y + 5.0), L.kl_full_distribution(x, y), atol=2e-5)
+
+
+def test_rowstats_oracle_ignore_index_and_neg_inf():
+    """cross_entropy's ignore_index -100 gives log-prob -0.0; a -inf logit
+    makes the reference's entropy NaN (0 * -inf) but leaves log-probs finite."""
+    from oracle import logprob_oracle as L
+    x = torch.tensor([[0.5, -1.0, 2.0, float("-inf")]])
+    lp = L.token_logprobs_from_logits(x, torch.tensor([-100]))
+    assert float(lp[0]) == 0.0 and str(float(lp[0])) == "-0.0"
+    assert torch.isnan(L.entropy_from_logits(x)).all()
+    assert torch.isfinite(L.token_logprobs_from_logits(x, torch.tensor([2]))).all()
