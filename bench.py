@@ -202,6 +202,75 @@ def bench_spec(args, dev) -> int:
     return 0
 
 
+def bench_rowstats(args, dev) -> int:
+    """Full-distribution statistics of RL training: one step = the token
+    log-probabilities and entropies of R positions of V-wide logits
+    (rowstats_<dtype>_<R>x<V>; "_kl" adds KL to a reference model's logits,
+    a second input of the same size)."""
+    import torch
+
+    from oracle import logprob_oracle as L
+    from rl_project_amd import row_stats
+
+    parts = args.workload.split("_")
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[parts[1]]
+    R, V = (int(v) for v in parts[2].split("x"))
+    kl = parts[-1] == "kl"
+    esz = torch.empty(0, dtype=dt).element_size()
+    per_buf = R * V * esz * (2 if kl else 1)
+    nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / per_buf))
+    bufs = []
+    for s in range(nbuf):
+        g = torch.Generator(device=dev).manual_seed(s)
+        x = (2.5 * torch.randn(R, V, generator=g, device=dev)).to(dt)
+        y = (x.float() + 0.5 * torch.randn(R, V, generator=g, device=dev)).to(dt) if kl else None
+        lab = torch.randint(0, V, (R,), generator=g, device=dev)
+        bufs.append((x, y, lab))
+    launch = lambda k: row_stats(bufs[k % nbuf][0], bufs[k % nbuf][2], bufs[k % nbuf][1], entropy=True,  # noqa: E731
+                                 check_labels=False)
+    stream = torch.cuda.current_stream(dev)
+    for i in range(max(args.warmup, nbuf)):
+        launch(i)
+    torch.cuda.synchronize(dev)
+    K = args.steps
+    kern_ms, wall = _timed_region(torch, dev, stream, K, launch)
+    durs = _isolated_launches(torch, dev, stream, launch)
+    alg_bytes = per_buf + R * (8 + 4 + 4 + (4 if kl else 0))
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    result = {
+        "metric": f"token log-prob + entropy{' + KL' if kl else ''} rows/sec over {R}x{V} {parts[1]} logits",
+        "value": R * K / wall, "unit": "rows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / K, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": parts[1], "data": "synthetic",
+        "config": {"workload": args.workload, "rows": R, "vocab": V, "kl": kl, "input_buffers": nbuf},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(args.workload),
+                     "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
+                     "isolated_launch_ms_p10": durs[len(durs) // 10],
+                     "isolated_launch_ms_p90": durs[(9 * len(durs)) // 10],
+                     "kernel": f"k_row_stats<{ {'bf16': 'BF16', 'f16': 'F16', 'f32': 'F32'}[parts[1]] }, {str(kl).lower()}>"},
+    }
+    if not args.no_cpu_baseline:
+        # the oracle (the reference's torch expressions) on the host, on the first rows
+        x, y, lab = (t.cpu() if t is not None else None for t in bufs[0])
+        rows = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            b = (rows % R)
+            L.token_logprobs_from_logits(x[b:b + 16], lab[b:b + 16])
+            L.entropy_from_logits(x[b:b + 16])
+            if kl:
+                L.kl_full_distribution(x[b:b + 16], y[b:b + 16])
+            rows += 16
+        dt_cpu = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": rows / dt_cpu, "unit": "rows/s", "cores": torch.get_num_threads(),
+                                  "kind": "port", "sample": f"{rows} rows in 16-row calls of the oracle's "
+                                  f"restatement (torch {torch.__version__} CPU, {torch.get_num_threads()} threads), "
+                                  f"{dt_cpu:.1f} s"}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +311,8 @@ def main() -> int:
         return 0
     if args.workload.startswith("spec_"):
         return bench_spec(args, dev)
+    if args.workload.startswith("rowstats_"):
+        return bench_rowstats(args, dev)
     w = workloads.make(args.workload, seed=0)
     batch_bytes = w.logits.numel() * w.logits.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))

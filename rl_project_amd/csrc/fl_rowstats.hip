@@ -30,6 +30,8 @@ namespace {
 constexpr int NT_RS = 256;
 constexpr int NW_RS = NT_RS / WAVE;
 constexpr int U_RS = 4;  // chunks per thread in flight
+constexpr float LOG2E_F = 1.44269504088896340736f;
+constexpr double LN2_D = 0.69314718055994530942;
 
 template <class D>
 struct RowChunk;
@@ -171,7 +173,8 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
     }
 #pragma unroll
     for (int k = 0; k < U_RS; ++k) {
-      // chunk maxima first: at most one re-base per chunk
+      const int c = c0 + k * NT_RS + tid;
+      // chunk maxima first: at most one re-base per chunk (padding is -inf)
       float cm = xs[k][0], cmy = ys[k][0];
 #pragma unroll
       for (int e = 1; e < N; ++e) {
@@ -180,27 +183,47 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
       }
       if (cm > acc.m) rebase_x(acc, cm);
       if (KL && cmy > acc.my) rebase_y(acc, cmy);
+      // exponents in base 2: d2 = (x - m) log2(e) in one rounding; the base-2
+      // sums are scaled to natural units once per chunk
+      const float mb = acc.m * LOG2E_F, myb = acc.my * LOG2E_F;
       float fs = 0.0f, fu = 0.0f, fsy = 0.0f, fw = 0.0f;
+      if (c < nfull && acc.m != -__builtin_inff() && (!KL || acc.my != -__builtin_inff())) {
+        // a whole chunk under a finite maximum: -inf gives d2 = -inf, e = 0
+        // and e * d2 = NaN, the reference's 0 * -inf
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        if (N * (c0 + k * NT_RS + tid) + e >= V) continue;  // padding past the row
-        // a -inf logit is -inf below any maximum, also below a maximum that
-        // is still -inf (where the subtraction would give NaN)
-        const float dx = xs[k][e] == -__builtin_inff() ? -__builtin_inff() : xs[k][e] - acc.m;
-        const float ex = __expf(dx);
-        fs += ex;
-        fu += ex * dx;
-        if (KL) {
-          const float dy = ys[k][e] == -__builtin_inff() ? -__builtin_inff() : ys[k][e] - acc.my;
-          fsy += __expf(dy);
-          fw += ex * (dx - dy);
+        for (int e = 0; e < N; ++e) {
+          const float d2 = fmaf(xs[k][e], LOG2E_F, -mb);
+          const float ex = __builtin_amdgcn_exp2f(d2);
+          fs += ex;
+          fu = fmaf(ex, d2, fu);
+          if (KL) {
+            const float dy2 = fmaf(ys[k][e], LOG2E_F, -myb);
+            fsy += __builtin_amdgcn_exp2f(dy2);
+            fw = fmaf(ex, d2 - dy2, fw);
+          }
+        }
+      } else {
+        // the row's last, partial chunk, chunks past the row, and values
+        // before any finite one (-inf below a maximum that is still -inf)
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          if (N * c + e >= V) continue;
+          const float d2 = xs[k][e] == -__builtin_inff() ? -__builtin_inff() : fmaf(xs[k][e], LOG2E_F, -mb);
+          const float ex = __builtin_amdgcn_exp2f(d2);
+          fs += ex;
+          fu += ex * d2;
+          if (KL) {
+            const float dy2 = ys[k][e] == -__builtin_inff() ? -__builtin_inff() : fmaf(ys[k][e], LOG2E_F, -myb);
+            fsy += __builtin_amdgcn_exp2f(dy2);
+            fw += ex * (d2 - dy2);
+          }
         }
       }
       acc.s += fs;
-      acc.u += fu;
+      acc.u += static_cast<double>(fu) * LN2_D;
       if (KL) {
         acc.sy += fsy;
-        acc.w += fw;
+        acc.w += static_cast<double>(fw) * LN2_D;
       }
     }
   }
