@@ -201,3 +201,96 @@ class SpeculativeGenerator:
     @property
     def acceptance_rate(self) -> float:
         return self.stats["accepted"] / max(self.stats["proposed"], 1)
+
+
+class MTPSpeculativeGenerator:
+    """Self-speculative decoding with the model's multi-token-prediction heads
+    (reference ``speculative.py:94-158``), one sequence.
+
+    Per round, as the reference:
+
+    1. ``token_1`` is sampled from the main head.
+    2. Each MTP head drafts the next token from the last hidden state and the
+       previous token's embedding.
+    3. ``token_1`` is appended.
+    4. The drafts are verified against one forward pass over the extended
+       sequence: accept while ``u < min(1, p/q)``; the first rejection
+       resamples ``max(0, p − q)``. A round draws no bonus token.
+
+    Filtering is the reference's ``_topk_filter(logits / T, top_k)``. Draws
+    are the build's inverse CDF with uniforms from ``generator``; the draws
+    and the verify run on the GPU path.  Model protocol: ``model(idx) ->
+    (logits, _)`` setting ``model._last_hidden``; ``model.full_logits``,
+    ``model.mtp_modules``, ``model.transformer.wte``, ``model.lm_head``,
+    ``model.spec.block_size``."""
+
+    def __init__(self, model):
+        if getattr(model, "mtp_modules", None) is None or len(model.mtp_modules) == 0:
+            raise ValueError("MTPSpeculativeGenerator requires a model with n_predict_tokens > 1")
+        self.model = model
+        self.n_drafts = len(model.mtp_modules)
+
+    @torch.no_grad()
+    def generate(self, idx: torch.Tensor, max_new_tokens: int = 200, temperature: float = 1.0,
+                 top_k: Optional[int] = 50, generator: Optional[torch.Generator] = None) -> torch.Tensor:
+        if idx.size(0) != 1:
+            raise ValueError("MTPSpeculativeGenerator.generate grows one sequence")
+        self.model.eval()
+        T = max(float(temperature), 1e-8)
+        k = top_k if (top_k is not None and top_k > 0) else 0
+        dev = idx.device
+        block = self.model.spec.block_size
+        generated = 0
+
+        def draw(row: torch.Tensor) -> torch.Tensor:
+            u = torch.rand(1, device=dev, generator=generator)
+            return sample_tokens(row, temperature=T, top_k=k, uniforms=u).tokens.view(1, 1)
+
+        while generated < max_new_tokens:
+            ctx = idx if idx.size(1) <= block else idx[:, -block:]
+            logits, _ = self.model(ctx)
+            last_h = self.model._last_hidden
+            main_row = logits[:, -1, :]
+            token_1 = draw(main_row)
+            draft_tokens, draft_rows = [token_1], [main_row]
+            prev_emb = self.model.transformer.wte(token_1)
+            for mtp_mod in self.model.mtp_modules:
+                h_mtp = mtp_mod(last_h[:, -1:, :], prev_emb)
+                row = self.model.lm_head(h_mtp[:, -1, :])
+                tok = draw(row)
+                draft_tokens.append(tok)
+                draft_rows.append(row)
+                prev_emb = self.model.transformer.wte(tok)
+
+            idx = torch.cat([idx, token_1], dim=1)
+            generated += 1
+            if generated >= max_new_tokens:
+                break
+            K = len(draft_tokens) - 1
+            if K > 0:
+                verify_idx = torch.cat([idx, torch.cat(draft_tokens[1:], dim=1)], dim=1)
+                if verify_idx.size(1) > block:
+                    verify_idx = verify_idx[:, -block:]
+                verify_logits = self.model.full_logits(verify_idx)
+                prompt_len = idx.size(1)
+                offset = verify_idx.size(1) - (prompt_len + K)
+                first = prompt_len - 1 + offset
+                if first < 0 or first + K >= verify_logits.size(1):
+                    # fewer verify positions than drafts (the context window cut them)
+                    if idx.size(1) >= block:
+                        break
+                    continue
+                # positions first .. first + K - 1 verify drafts 1..K; position
+                # first + K would be the bonus, which this scheme does not draw
+                out = speculative_verify(verify_logits[:, first:first + K + 1, :].contiguous(),
+                                         torch.stack(draft_rows[1:], dim=1).to(verify_logits.dtype),
+                                         torch.cat(draft_tokens[1:], dim=1), temperature=T, top_k=k or None,
+                                         generator=generator)
+                n = int(out.n_accepted[0])
+                new = out.tokens[0, : (n if n == K else n + 1)]
+                new = new[: max_new_tokens - generated]
+                idx = torch.cat([idx, new.view(1, -1)], dim=1)
+                generated += new.numel()
+            if idx.size(1) >= block:
+                break
+        return idx
