@@ -19,12 +19,13 @@ from .params import GenerationSettings, SamplingParams, SamplingParamsError
 from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, describe_rows, filtered_outputs,
                        generate_tokens, sample_from_logits, sample_tokens)
 from .speculative import MTPSpeculativeGenerator, SpeculativeGenerator, SpecOutput, SpecPlan, speculative_verify
+from .engine import BatchedSampler
 from .logprobs import RowStats, entropy_from_logits, kl_full_distribution, row_stats, token_logprobs_from_logits
 
 __all__ = [
     "apply_sampling_filters", "sample_from_logits", "generate_tokens",
     "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplingError",
     "speculative_verify", "SpeculativeGenerator", "MTPSpeculativeGenerator", "SpecOutput", "SpecPlan",
-    "row_stats", "RowStats", "token_logprobs_from_logits", "entropy_from_logits", "kl_full_distribution",
+    "BatchedSampler", "row_stats", "RowStats", "token_logprobs_from_logits", "entropy_from_logits", "kl_full_distribution",
     "SamplingParams", "GenerationSettings", "SamplingParamsError",
 ]

@@ -77,6 +77,17 @@ def _history_tensor(history, B: int, V: int, device: torch.device) -> Tuple[Opti
     """Pack per-row histories into ([B, H] int32, [B] int32 lengths, row stride)."""
     if history is None:
         return None, None, 0
+    if (isinstance(history, tuple) and len(history) == 2 and isinstance(history[0], torch.Tensor)
+            and isinstance(history[1], torch.Tensor)):
+        # device-resident (ids [B, H] int32, lengths [B] int32): used as they are
+        h, lens = history
+        if h.dim() != 2 or h.size(0) != B or lens.numel() != B or h.dtype != torch.int32 or lens.dtype != torch.int32:
+            raise ValueError("history (ids, lengths) must be int32 [B, H] and int32 [B]")
+        if h.size(1) > _lib.FL_MAX_HISTORY:
+            raise NotImplementedError(f"history of {h.size(1)} ids exceeds {_lib.FL_MAX_HISTORY}")
+        if h.stride(1) != 1:
+            h = h.contiguous()
+        return h, lens.contiguous(), h.stride(0) if B > 1 else h.size(1)
     if isinstance(history, torch.Tensor):
         h = history.to(device=device, dtype=torch.int32)
         if h.dim() == 1:
@@ -234,7 +245,8 @@ def sample_tokens(
 
     Per-row parameters accept a scalar, a sequence (None entries mean "off") or
     a device tensor.  ``history``: per-row token-id lists (or a [B, H] / [H]
-    tensor) for the repetition penalty; ``stop_ids``: one shared list, per-row
+    tensor, or a device-resident pair (ids int32 [B, H], lengths int32 [B]))
+    for the repetition penalty; ``stop_ids``: one shared list, per-row
     lists, or a [S] / [B, S] tensor; ``uniforms``: float32 [B] in [0, 1).
     Equivalent to ``engine.py:118-127`` applied to every row: the filtered
     logits of ``apply_sampling_filters``, ``sample_from_logits``, the stop test
