@@ -29,7 +29,6 @@ namespace {
 
 constexpr int NT_RS = 256;
 constexpr int NW_RS = NT_RS / WAVE;
-constexpr int U_RS = 4;  // chunks per thread in flight
 constexpr float LOG2E_F = 1.44269504088896340736f;
 constexpr double LN2_D = 0.69314718055994530942;
 
@@ -136,6 +135,7 @@ template <class D, bool KL>
 __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) {
   using C = RowChunk<D>;
   constexpr int N = C::N;
+  constexpr int U_RS = 4;  // chunks per thread in flight (8 lowers the occupancy and the bandwidth)
   __shared__ Acc part[NW_RS];
   const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;
@@ -171,25 +171,29 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
         for (int e = 0; e < N; ++e) xs[k][e] = ys[k][e] = -__builtin_inff();
       }
     }
+    // maxima of the iteration's chunks first: at most one re-base per
+    // iteration (padding is -inf)
+    float cm = xs[0][0], cmy = ys[0][0];
 #pragma unroll
-    for (int k = 0; k < U_RS; ++k) {
-      const int c = c0 + k * NT_RS + tid;
-      // chunk maxima first: at most one re-base per chunk (padding is -inf)
-      float cm = xs[k][0], cmy = ys[k][0];
+    for (int k = 0; k < U_RS; ++k)
 #pragma unroll
-      for (int e = 1; e < N; ++e) {
+      for (int e = 0; e < N; ++e) {
         cm = fmaxf(cm, xs[k][e]);
         if (KL) cmy = fmaxf(cmy, ys[k][e]);
       }
-      if (cm > acc.m) rebase_x(acc, cm);
-      if (KL && cmy > acc.my) rebase_y(acc, cmy);
-      // exponents in base 2: d2 = (x - m) log2(e) in one rounding; the base-2
-      // sums are scaled to natural units once per chunk
-      const float mb = acc.m * LOG2E_F, myb = acc.my * LOG2E_F;
-      float fs = 0.0f, fu = 0.0f, fsy = 0.0f, fw = 0.0f;
-      if (c < nfull && acc.m != -__builtin_inff() && (!KL || acc.my != -__builtin_inff())) {
-        // a whole chunk under a finite maximum: -inf gives d2 = -inf, e = 0
-        // and e * d2 = NaN, the reference's 0 * -inf
+    if (cm > acc.m) rebase_x(acc, cm);
+    if (KL && cmy > acc.my) rebase_y(acc, cmy);
+    // exponents in base 2: d2 = (x - m) log2(e) in one rounding; the base-2
+    // sums of the iteration (at most U_RS * N terms, each at most 1) are
+    // scaled to natural units and added to the float64 partials once
+    const float mb = acc.m * LOG2E_F, myb = acc.my * LOG2E_F;
+    float fs = 0.0f, fu = 0.0f, fsy = 0.0f, fw = 0.0f;
+    const bool finite_max = acc.m != -__builtin_inff() && (!KL || acc.my != -__builtin_inff());
+    if (c0 + (U_RS - 1) * NT_RS + tid < nfull && finite_max) {
+      // whole chunks under a finite maximum: -inf gives d2 = -inf, e = 0 and
+      // e * d2 = NaN, the reference's 0 * -inf
+#pragma unroll
+      for (int k = 0; k < U_RS; ++k)
 #pragma unroll
         for (int e = 0; e < N; ++e) {
           const float d2 = fmaf(xs[k][e], LOG2E_F, -mb);
@@ -202,9 +206,12 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
             fw = fmaf(ex, d2 - dy2, fw);
           }
         }
-      } else {
-        // the row's last, partial chunk, chunks past the row, and values
-        // before any finite one (-inf below a maximum that is still -inf)
+    } else {
+      // the row's last chunks (partial or past the row) and values before any
+      // finite one (-inf below a maximum that is still -inf)
+#pragma unroll
+      for (int k = 0; k < U_RS; ++k) {
+        const int c = c0 + k * NT_RS + tid;
 #pragma unroll
         for (int e = 0; e < N; ++e) {
           if (N * c + e >= V) continue;
@@ -219,12 +226,12 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
           }
         }
       }
-      acc.s += fs;
-      acc.u += static_cast<double>(fu) * LN2_D;
-      if (KL) {
-        acc.sy += fsy;
-        acc.w += static_cast<double>(fw) * LN2_D;
-      }
+    }
+    acc.s += fs;
+    acc.u += static_cast<double>(fu) * LN2_D;
+    if (KL) {
+      acc.sy += fsy;
+      acc.w += static_cast<double>(fw) * LN2_D;
     }
   }
   // merge: wave tree, then the waves in order
