@@ -498,8 +498,33 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
     atomicAdd(reinterpret_cast<unsigned long long*>(&sh.acc[ok ? b : NBF]),
               static_cast<unsigned long long>(ok ? w : 0ull));
   };
+  // A chunk of 4 whose values are all valid, finite and inside the bins (the
+  // usual case) needs no per-element test: its maximum, minimum and sum
+  // (NaN if any value is) decide it once; any other chunk goes element by
+  // element.  (fmaxf / fminf skip NaN, the sum does not.)
+  auto add4 = [&](int ch, const float (&y)[4]) __attribute__((always_inline)) {
+    const float mx = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+    const float mn = fminf(fminf(y[0], y[1]), fminf(y[2], y[3]));
+    const float sm = (y[0] + y[1]) + (y[2] + y[3]);
+    if (4 * ch + 3 < V && mx <= c && mn > -__builtin_inff() && sm == sm) {
+      km = max(km, f32_key(mx));
+      nfin += 4u;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) add(4 * ((j >> 2) * NT + tid) + (j & 3), yb[j]);
+      for (int e = 0; e < 4; ++e) {
+        const int b = fbin(y[e], c);
+        const uint64_t w = (1ull << CNT_SH) | fterm(y[e], b, c);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&sh.acc[b]), static_cast<unsigned long long>(w));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) add(4 * ch + e, y[e]);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float y4[4] = {yb[4 * u], yb[4 * u + 1], yb[4 * u + 2], yb[4 * u + 3]};
+    add4(u * NT + tid, y4);
+  }
   const int nch = X.nch;
   for (int c0 = 4 * NT; c0 < nch; c0 += 4 * NT) {
     float4 q[4];
@@ -510,8 +535,10 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
       const int ch = c0 + u * NT + tid;
       const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+      float y4[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) add(4 * ch + e, X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u));
+      for (int e = 0; e < 4; ++e) y4[e] = X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u);
+      add4(ch, y4);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
