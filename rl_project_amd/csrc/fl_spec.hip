@@ -171,10 +171,8 @@ struct PairRows {
     nch = (V + N - 1) / N;
     nfull = V / N;
   }
-  // f(e, i, p_i, q_i) for the N elements of chunk c (ascending index i = N c + e)
-  template <class F>
-  __device__ __forceinline__ void chunk(int c, F&& f) const {
-    float xt[N], xd[N];
+  // the raw logits of chunk c of both rows
+  __device__ __forceinline__ void load(int c, float (&xt)[N], float (&xd)[N]) const {
     if (aligned && c < nfull) {
       C::unpack(buf_load16(rt, 16u * c, 0u), xt);
       C::unpack(buf_load16(rd, 16u * c, 0u), xd);
@@ -185,11 +183,21 @@ struct PairRows {
         xd[e] = C::elem(rd, N * c + e);
       }
     }
+  }
+  // f(e, i, p_i, q_i) for the N elements of chunk c (ascending index i = N c + e)
+  template <class F>
+  __device__ __forceinline__ void eval(int c, const float (&xt)[N], const float (&xd)[N], F&& f) const {
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       const int i = N * c + e;
       if (i < V) f(e, i, prob_of<D>(td, filt_value<D>(xt[e], cap, T), i), prob_of<D>(dd, filt_value<D>(xd[e], cap, T), i));
     }
+  }
+  template <class F>
+  __device__ __forceinline__ void chunk(int c, F&& f) const {
+    float xt[N], xd[N];
+    load(c, xt, xd);
+    eval(c, xt, xd, f);
   }
 };
 
@@ -210,12 +218,25 @@ struct Weight {
 };
 
 // Sum over chunks [c0, c1) of fx45(g(p, q)) by the calling thread, chunks
-// interleaved over nthreads threads (coalesced loads).
+// interleaved over nthreads threads (coalesced loads), four chunks of both
+// rows in flight per thread.
 template <class D, class G>
 __device__ __forceinline__ uint64_t range_sum(const PairRows<D>& R, int c0, int c1, int nthreads, G&& g) {
+  constexpr int U = 4;
   uint64_t acc = 0;
-  for (int c = c0 + static_cast<int>(threadIdx.x); c < c1; c += nthreads)
-    R.chunk(c, [&](int, int, float p, float q) { acc += fx45(g(p, q)); });
+  for (int cb = c0 + static_cast<int>(threadIdx.x); cb < c1; cb += U * nthreads) {
+    float xt[U][PairRows<D>::N], xd[U][PairRows<D>::N];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+      if (c < c1) R.load(c, xt[u], xd[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+      if (c < c1) R.eval(c, xt[u], xd[u], [&](int, int, float p, float q) { acc += fx45(g(p, q)); });
+    }
+  }
   return acc;
 }
 
