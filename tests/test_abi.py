@@ -165,3 +165,31 @@ def test_spec_workspace_bytes_and_checks():
     assert "workspace" in L.fl_last_error().decode()
     s.workspace, s.workspace_bytes = 0x2004, 1 << 20    # misaligned
     assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL
+
+
+def test_row_stats_argument_checks():
+    """fl_row_stats rejects bad arguments before any launch (no GPU needed)."""
+    L = _lib.lib()
+    assert L.fl_row_stats(None, None) == _lib.FL_EINVAL
+    a = _lib.RowStatsArgs()
+    a.struct_size = ctypes.sizeof(_lib.RowStatsArgs) - 8
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
+    assert "struct_size" in L.fl_last_error().decode()
+    a.struct_size = ctypes.sizeof(_lib.RowStatsArgs)
+    a.dtype, a.rows, a.vocab, a.ld, a.logits = 1, 4, 1000, 1000, 0x1000
+    a.out_kl = 0x2000                       # KL without a reference row
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
+    assert "ref_logits" in L.fl_last_error().decode()
+    a.out_kl = None
+    a.out_logprob = 0x2000                  # log-probs without labels
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
+    assert "labels" in L.fl_last_error().decode()
+    a.out_logprob = None
+    a.ld = 999                              # row stride below the vocabulary
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
+    a.ld, a.vocab = (1 << 25), (1 << 25)    # beyond the build's row length
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_ENOTSUP
+    a.vocab, a.ld, a.dtype = 1000, 1000, 9  # unknown dtype
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
+    a.dtype, a.rows = 1, 0                  # nothing to do
+    assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_OK

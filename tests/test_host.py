@@ -106,3 +106,39 @@ def test_bench_refuses_several_gpus():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_logprob_entry_points_need_device_tensors_and_matching_shapes():
+    from rl_project_amd import entropy_from_logits, kl_full_distribution, row_stats, token_logprobs_from_logits
+    x = torch.zeros(2, 3, 10)
+    with pytest.raises(ValueError, match="ROCm"):
+        entropy_from_logits(x)
+    with pytest.raises(ValueError, match="ROCm"):
+        token_logprobs_from_logits(x, torch.zeros(2, 3, dtype=torch.long))
+    with pytest.raises(ValueError, match="ROCm"):
+        kl_full_distribution(x, x)
+    with pytest.raises(ValueError, match="ROCm"):    # the device is checked first
+        row_stats(torch.zeros(2, 10, dtype=torch.float64), entropy=True)
+
+
+def test_spec_plan_checks_shapes_before_any_launch():
+    from rl_project_amd import SpecPlan
+    t, d = torch.zeros(2, 4, 16), torch.zeros(2, 3, 16)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        SpecPlan(t, d, torch.zeros(2, 2, dtype=torch.long))
+    with pytest.raises(ValueError, match="must be"):
+        SpecPlan(torch.zeros(4, 16), d, torch.zeros(2, 3, dtype=torch.long))
+    with pytest.raises(ValueError, match="dtype"):
+        SpecPlan(t, d.double(), torch.zeros(2, 3, dtype=torch.long))
+
+
+def test_history_pair_validation():
+    from rl_project_amd.sampling import _history_tensor
+    ids = torch.zeros(3, 8, dtype=torch.int32)
+    lens = torch.full((3,), 4, dtype=torch.int32)
+    h, l, ld = _history_tensor((ids, lens), 3, 100, torch.device("cpu"))
+    assert h is ids and ld == 8 and torch.equal(l, lens)
+    with pytest.raises(ValueError):
+        _history_tensor((ids.long(), lens), 3, 100, torch.device("cpu"))
+    with pytest.raises(ValueError):
+        _history_tensor((ids, lens[:2]), 3, 100, torch.device("cpu"))
