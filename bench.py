@@ -77,8 +77,11 @@ def _isolated_launches(torch, dev, stream, launch, n: int = ISOLATED):
 
 def cpu_baseline(w, seconds: float):
     """The oracle's per-row restatement (one [1, V] call per row, as the
-    reference inference engine makes them) on the first rows of the workload,
-    until ``seconds`` of CPU time have been spent."""
+    reference inference engine makes them) on the first rows of the workload:
+    the median rate of three segments of ``seconds / 3`` with all the threads
+    torch uses, and one segment of ``seconds / 3`` on a single thread."""
+    import statistics
+
     import torch
 
     from oracle import sampler_oracle as O
@@ -94,17 +97,32 @@ def cpu_baseline(w, seconds: float):
     params = [row_params(w, b) for b in range(w.batch)]
     # one warm-up row, then rows 0, 1, ... (cycling through the batch) until the time is spent
     O.sample_rows(x[:1], params[:1], u[:1], softcap=w.softcap, want_filtered=False)
-    rows = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        b = rows % w.batch
-        O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap, want_filtered=False)
-        rows += 1
-    dt = time.perf_counter() - t0
-    return {"value": rows / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{rows} rows of {w.name} (seed 0, cycling through its {w.batch} rows), one [1,V] oracle call per row "
-                      f"(torch {torch.__version__} CPU, {torch.get_num_threads()} threads, "
-                      f"{torch.backends.cpu.get_cpu_capability()}), {dt:.1f} s"}
+    state = {"row": 0}
+
+    def segment(sec: float) -> float:
+        rows = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < sec:
+            b = state["row"] % w.batch
+            O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap, want_filtered=False)
+            state["row"] += 1
+            rows += 1
+        return rows / (time.perf_counter() - t0)
+
+    threads = torch.get_num_threads()
+    rates = [segment(seconds / 3.0) for _ in range(3)]
+    torch.set_num_threads(1)
+    try:
+        one = segment(seconds / 3.0)
+    finally:
+        torch.set_num_threads(threads)
+    return {"value": statistics.median(rates), "unit": "rows/s", "cores": threads, "kind": "port",
+            "single_thread_value": one,
+            "sample": f"{state['row']} rows of {w.name} (seed 0, cycling through its {w.batch} rows), one [1,V] "
+                      f"oracle call per row (torch {torch.__version__} CPU, ATEN_CPU_CAPABILITY "
+                      f"{torch.backends.cpu.get_cpu_capability()}); value: median of 3 segments of "
+                      f"{seconds / 3:.1f} s on {threads} threads ({', '.join(f'{r:.1f}' for r in rates)} rows/s); "
+                      f"single_thread_value: one segment of {seconds / 3:.1f} s on 1 thread"}
 
 
 def cpu_baseline_spec(w, seconds: float):
@@ -278,7 +296,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD)
     ap.add_argument("--buffers", type=int, default=0, help="distinct input batches (default: > 256 MB in total)")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time (3 segments; a fourth on 1 thread)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run an elementwise read+write kernel (torch.neg) over MIB MiB, 5 launches: the "
