@@ -42,7 +42,7 @@ constexpr int HPRE = 2;                          // history ids per thread loade
 static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
 
 struct Shared16 {
-  uint32_t hist[HIST_WORDS];
+  uint32_t hist[HIST_WORDS + WAVE];  // pattern counts, then one -inf counter per lane
   uint32_t hbits[HBITS_WORDS];
   uint32_t owner[OWNER_WORDS];
   uint64_t redq[NWAVE];
@@ -234,6 +234,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   static_assert(HIST_WORDS == 8 * 4 * NT && HBITS_WORDS == 4 * NT && OWNER_WORDS <= 4 * NT, "LDS clear layout");
 #pragma unroll
   for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(sh.hist)[tid + k * NT] = make_uint4(0, 0, 0, 0);
+  if (tid < WAVE) sh.hist[HIST_WORDS + tid] = 0;
   reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
   if (tid < OWNER_WORDS / 4) reinterpret_cast<uint4*>(sh.owner)[tid] = make_uint4(0, 0, 0, 0);
   if (tid < 2 * NCH) (&sh.slot[0][0])[tid] = 0;
@@ -310,7 +311,16 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
 
   // ------------------------------------------------ count patterns
-  auto count = [&](uint32_t bits) { atomicAdd(&sh.hist[bits >> 1], 1u + (bits & 1u) * 0xFFFFu); };
+  // -inf values (a masked vocabulary) are never kept, selected or weighted:
+  // they stay out of the pattern counts, where more than 65535 of them would
+  // wrap a 16-bit counter, and go to a 32-bit counter of this lane past the
+  // patterns (the -inf pattern is even, so its increment is 1).  With a
+  // per-entry soft-cap a raw -inf becomes -cap and is counted by its pattern.
+  const uint32_t neg_inf_bits = sc_entry ? 0xFFFFFFFFu : (0x8000u | D::INF_BITS);
+  const uint32_t inf_word = HIST_WORDS + (tid & (WAVE - 1));
+  auto count = [&](uint32_t bits) {
+    atomicAdd(&sh.hist[bits == neg_inf_bits ? inf_word : bits >> 1], 1u + (bits & 1u) * 0xFFFFu);
+  };
   if (fast) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -478,8 +488,15 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   auto cnt_of = [&](int i) -> uint32_t { return ent[i] & 0xFFFFu; };
   auto y_raw = [&](int i) -> float { return y_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry); };
   const float M = N > 0 ? y_raw(0) : 0.0f;
+  // -inf values of the row (read where a total is off or nothing is left)
+  auto neg_inf_count = [&]() -> uint32_t {
+    uint32_t n = 0;
+    for (int l = 0; l < WAVE; ++l) n += sh.hist[HIST_WORDS + l];
+    return n;
+  };
   if (tid == 0) {
-    if (N == 0 || isnan(M)) sh.status |= FL_ROW_NAN;
+    if (N == 0) sh.status |= neg_inf_count() == static_cast<uint32_t>(V) ? FL_ROW_ALL_MASKED : FL_ROW_NAN;
+    else if (isnan(M)) sh.status |= FL_ROW_NAN;
     else if (isinf(M)) sh.status |= (M > 0.0f) ? FL_ROW_INF : FL_ROW_ALL_MASKED;
   }
   auto Y = [&](int i) -> float { return cached ? Yc[i] : y_raw(i); };
@@ -516,8 +533,10 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         Cm[N] = tm;
       }
     }
-    // a total other than V means a 16-bit counter wrapped (> 65535 equal values)
-    if (tid == 0 && tc != static_cast<uint32_t>(V)) atomicOr(&sh.status, FL_ROW_LIMIT);
+    // a total other than V less the -inf values means a 16-bit counter
+    // wrapped (> 65535 equal values)
+    if (tid == 0 && tc != static_cast<uint32_t>(V) && tc + neg_inf_count() != static_cast<uint32_t>(V))
+      atomicOr(&sh.status, FL_ROW_LIMIT);
   }
   __syncthreads();
   int32_t status = sh.status;
@@ -569,7 +588,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       if (K > 0 && K < V) {
         // first entry whose inclusive count reaches K; every equal value stays
         const int ik = wave_first(0, N, [&](int i) { return count_before(i + 1) >= static_cast<uint32_t>(K); });
-        L = group_hi(ik, Y(ik)) + 1;
+        // (k beyond the finite values: the k-th largest is -inf, every
+        // finite value stays)
+        if (ik < N) L = group_hi(ik, Y(ik)) + 1;
       }
       double S = from_fx(mass_before(L));
       if (MP > 0.0f) {
