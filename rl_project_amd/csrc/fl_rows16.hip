@@ -38,6 +38,7 @@ constexpr int CACHE_MAX = (SLICE_BASE - 4) / 6;   // entries with y, e, prefix c
 constexpr int NSTEP = 512;                        // compaction steps of 128 orders
 constexpr int SPW = NSTEP / NWAVE;                // steps per wave
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
+constexpr int EARLY_CHUNKS = 2;                  // row chunks per thread requested before the LDS clear
 
 static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
 
@@ -60,7 +61,7 @@ struct Shared16 {
     uint32_t o_lo[2], o_hi[2];
     float y_sel, y_cut;
   } dec;  // results of the search wave
-  uint32_t slot[2][NCH];  // identification: members per slot of NT chunks
+  uint32_t wc[2][NCH][NWAVE];  // identification: members per slot of NT chunks and wave
   uint32_t nh[2];         // identification: history members
 };
 
@@ -225,11 +226,21 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     const int i = tid + k * NT;
     hpre[k] = hpre_src[hist_rows ? min(i, static_cast<int>(a.hist_ld) - 1) : 0];
   }
+  // The first EARLY_CHUNKS chunks of the row tile are requested before the
+  // LDS clear, so that the row starts to stream in during it; the rest after
+  // the clear's barrier: a wave stalls in issuing its loads until the memory
+  // system accepts them (at the HBM rate), so a barrier placed after all of
+  // them would only open once most of the row had arrived.
+  const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast ? 2u * static_cast<uint32_t>(V) : 0u);
+  uint4 d[NCH];
+#pragma unroll
+  for (int j = 0; j < EARLY_CHUNKS; ++j) {
+    d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // ------------------------------------------------ clear LDS
-  // Before the row loads: a wave stalls in issuing its loads until the memory
-  // system accepts them (at the HBM rate), so a barrier placed after them
-  // would only open once the whole row had arrived.  Straight-line stores: a
-  // loop here makes the compiler wait for outstanding loads.
+  // Straight-line stores: a loop here makes the compiler wait for
+  // outstanding loads.
   FL_MARK(0);  // (after the parameter loads: a mark before them makes the tuning build spill)
   static_assert(HIST_WORDS == 8 * 4 * NT && HBITS_WORDS == 4 * NT && OWNER_WORDS <= 4 * NT, "LDS clear layout");
 #pragma unroll
@@ -237,7 +248,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   if (tid < WAVE) sh.hist[HIST_WORDS + tid] = 0;
   reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
   if (tid < OWNER_WORDS / 4) reinterpret_cast<uint4*>(sh.owner)[tid] = make_uint4(0, 0, 0, 0);
-  if (tid < 2 * NCH) (&sh.slot[0][0])[tid] = 0;
+  static_assert(2 * NCH * NWAVE <= NT, "one member counter per thread to clear");
+  if (tid < 2 * NCH * NWAVE) (&sh.wc[0][0][0])[tid] = 0;
   if (tid == 0) {
     sh.status = 0;
     sh.nh[0] = sh.nh[1] = 0;
@@ -260,13 +272,11 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // (unconditional: behind a branch, the compiler's wait for the history ids
   // would also wait for the row on the path that loaded it; a row the fast
   // path does not take gets an empty range, so its loads return zeros)
-  const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast ? 2u * static_cast<uint32_t>(V) : 0u);
   // (issued in chunk order, pinned by scheduling barriers: the count pass
   // takes the chunks in that order, and counting a chunk whose load was issued
   // late would hold back the counting of all chunks after it)
-  uint4 d[NCH];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
+  for (int j = EARLY_CHUNKS; j < NCH; ++j) {
     d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -840,48 +850,71 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         rlo[2 * t + 1] = 0x8000u, rw[2 * t + 1] = o_hi[t] - 0x8000u, ren[2 * t + 1] = true;
       }
     }
-    // Per chunk, branch-free, the members of each range: for a half
-    // d = w - lo, min(d, 0x8000) - (width + 1) has its top bit set iff
-    // d <= width (width + 1 <= 0x8000); the shifted-down top bits summed
-    // over the chunk's words count its members.  (Written as instructions:
-    // the compiler would turn the arithmetic back into compares.)
-    const uint32_t c8000 = 0x80008000u, c15 = 0x000F000Fu;
+    // Members per slot j and wave w (chunks j * NT + 64 w .. + 63).  For a
+    // word of two patterns, e = max(w - lo - width, 0) per half (wrapping
+    // subtraction, then a clamped one) is zero exactly for a member; the
+    // minimum over the chunk's words and both ranges flags a chunk holding
+    // any.  Chunks rarely hold one, so the exact count (min(e, 1) summed over
+    // the halves counts the non-members) runs only where a lane of the wave
+    // has a flagged chunk.  (Written as instructions: the compiler would turn
+    // the packed arithmetic back into compares.)
+    const int wv = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int lane_id = tid & (WAVE - 1);
+    // the partial chunk (V not a multiple of 8): its zero padding reads as
+    // the pattern of +0.0
+    const int pad = (nfull < nchunks) ? 8 - (V - nfull * 8) : 0;
+    const uint32_t ones2 = 0x00010001u;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
+      const bool zero_in = in_range(t, 0u);
+      const bool pad_in = pad > 0 && zero_in;
       if (fast) {
 #pragma unroll
         for (int j = 0; j < NCH; ++j) {
-          uint32_t acc = 0;
+          const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+          uint32_t m[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
 #pragma unroll
           for (int rr = 2 * t; rr < 2 * t + 2; ++rr) {
             if (!ren[rr]) continue;  // wave-uniform
-            const uint32_t lo2 = rlo[rr] * 0x10001u, th2 = (rw[rr] + 1u) * 0x10001u;
-            const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+            const uint32_t lo2 = rlo[rr] * 0x10001u, wd2 = rw[rr] * 0x10001u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              uint32_t f;
+              uint32_t e;
               asm("v_pk_sub_u16 %0, %1, %2\n\t"
-                  "v_pk_min_u16 %0, %0, %3\n\t"
-                  "v_pk_sub_u16 %0, %0, %4\n\t"
-                  "v_pk_lshrrev_b16 %0, %5, %0"
-                  : "=&v"(f)
-                  : "v"(w4[k]), "s"(lo2), "s"(c8000), "s"(th2), "s"(c15));
-              acc += f;  // halves count separately: at most 16 per half
+                  "v_pk_sub_u16 %0, %0, %3 clamp\n\t"
+                  "v_pk_min_u16 %0, %0, %4"
+                  : "=&v"(e)
+                  : "v"(w4[k]), "s"(lo2), "s"(wd2), "v"(m[k]));
+              m[k] = e;
             }
           }
-          uint32_t cj = (acc & 0xFFFFu) + (acc >> 16);
+          uint32_t mm, m23;
+          asm("v_pk_min_u16 %0, %1, %2" : "=v"(mm) : "v"(m[0]), "v"(m[1]));
+          asm("v_pk_min_u16 %0, %1, %2" : "=v"(m23) : "v"(m[2]), "v"(m[3]));
+          asm("v_pk_min_u16 %0, %0, %1" : "+v"(mm) : "v"(m23));
           const int c = j * NT + tid;
-          if (c >= nchunks) cj = 0;
-          else if (c == nfull && in_range(t, 0u)) cj -= static_cast<uint32_t>(8 - (V - c * 8));  // zero padding
-          if (cj) atomicAdd(&sh.slot[t][j], cj);
+          bool flag = ((mm & 0xFFFFu) == 0u) | (mm < 0x10000u);
+          // lanes past the row hold zeros, members only if +0.0 is a target
+          if (zero_in && (j + 1) * NT > nchunks) flag = flag && c < nchunks;
+          if (__ballot(flag) != 0ull) {  // wave-uniform
+            uint32_t f0, f1, f2, f3;
+            asm("v_pk_min_u16 %0, %1, %2" : "=v"(f0) : "v"(m[0]), "s"(ones2));
+            asm("v_pk_min_u16 %0, %1, %2" : "=v"(f1) : "v"(m[1]), "s"(ones2));
+            asm("v_pk_min_u16 %0, %1, %2" : "=v"(f2) : "v"(m[2]), "s"(ones2));
+            asm("v_pk_min_u16 %0, %1, %2" : "=v"(f3) : "v"(m[3]), "s"(ones2));
+            const uint32_t nm = f0 + f1 + f2 + f3;  // halves at most 4: no carry between them
+            uint32_t cj = flag ? 8u - ((nm & 0xFFFFu) + (nm >> 16)) : 0u;
+            if (pad_in && c == nfull) cj -= static_cast<uint32_t>(pad);
+            if (cj) atomicAdd(&sh.wc[t][j][wv], cj);
+          }
         }
       } else {
         for (int j = 0; j < NCH; ++j) {
           const int c = j * NT + tid;
           if (c >= nchunks) break;
           const uint32_t cj = static_cast<uint32_t>(__popc(chunk_mask(t, c, load_chunk16(row, c, V, ALIGNED))));
-          if (cj) atomicAdd(&sh.slot[t][j], cj);
+          if (cj) atomicAdd(&sh.wc[t][j][wv], cj);
         }
       }
     }
@@ -897,7 +930,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
           const bool mem = in_range(t, zp);
           // the packed count of the fast path took the id by its raw pattern
           const int corr = (mem ? 1 : 0) - ((fast && in_range(t, z)) ? 1 : 0);
-          if (corr != 0) atomicAdd(&sh.slot[t][(id >> 3) / NT], static_cast<uint32_t>(corr));
+          if (corr != 0) atomicAdd(&sh.wc[t][(id >> 3) / NT][((id >> 3) % NT) / WAVE], static_cast<uint32_t>(corr));
           if (mem) push(t, id);
         }
       };
@@ -917,45 +950,53 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       if (!active[t]) continue;
       const uint32_t n = sh.nh[t];
       if (n <= static_cast<uint32_t>(HLIST_CAP)) {
-        // the slot holding rank r, then a block scan of the members each
-        // thread holds there (its chunk's non-history members and the listed
-        // history members in its chunk)
-        int js = -1;
-        uint32_t rr = 0, run = 0;
+        // The (slot, wave) holding rank r, found by every wave alike: lane l
+        // reads the counts of slot l / 4, waves 4 (l % 4) .. + 3, which puts
+        // the lanes in index order; an inclusive scan over the lanes finds
+        // the lane, four compares the wave.  That wave alone then forms its
+        // lanes' members in the slot (the chunk's non-history members and
+        // the listed history members in the chunk) and scans them.
+        static_assert(NCH * NWAVE == 4 * WAVE, "four counters per lane");
+        const uint4 q4 = reinterpret_cast<const uint4*>(&sh.wc[t][0][0])[lane_id];
+        const uint32_t s4 = q4.x + q4.y + q4.z + q4.w;
+        const uint32_t inc = wave_incl_scan(s4);
+        const uint64_t hit = __ballot(inc > rank[t]);
+        if (hit != 0ull) {  // the same in every wave
+          const int L = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+          uint32_t rr = rank[t] - static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inc - s4), L));
+          const uint32_t qc[4] = {static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.x), L)),
+                                  static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.y), L)),
+                                  static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.z), L)),
+                                  static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.w), L))};
+          int kq = 0;
+          while (kq < 3 && rr >= qc[kq]) rr -= qc[kq++];
+          const int ws = 4 * (L & 3) + kq;
+          const int js = L >> 2;
+          if (wv == ws) {
+            const int c = js * NT + tid;
+            uint32_t b = 0;
+            if (c < nchunks) {
+              uint4 q = make_uint4(0, 0, 0, 0);
+              if (fast) {
 #pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-          const uint32_t tj = sh.slot[t][j];
-          if (js < 0 && rank[t] < run + tj) {
-            js = j;
-            rr = rank[t] - run;
-          }
-          run += tj;
-        }
-        if (js >= 0) {  // the same in every thread
-          const int c = js * NT + tid;
-          uint32_t b = 0;
-          if (c < nchunks) {
-            uint4 q = make_uint4(0, 0, 0, 0);
-            if (fast) {
-#pragma unroll
-              for (int j = 0; j < NCH; ++j)
-                if (j == js) q = r[j];  // js is wave-uniform
-            } else {
-              q = load_chunk16(row, c, V, ALIGNED);
+                for (int j = 0; j < NCH; ++j)
+                  if (j == js) q = r[j];  // js is wave-uniform
+              } else {
+                q = load_chunk16(row, c, V, ALIGNED);
+              }
+              b = chunk_mask(t, c, q);
             }
-            b = chunk_mask(t, c, q);
-          }
-          for (uint32_t k = 0; k < n; ++k) {
-            const int id = static_cast<int>(hlist[t][k]);
-            if ((id >> 3) == c) b |= 1u << (id & 7);
-          }
-          const uint32_t cb = static_cast<uint32_t>(__popc(b));
-          uint32_t tot;
-          const uint32_t ex = block_excl_scan<uint32_t>(cb, sh.redu, &tot);
-          if (ex <= rr && rr < ex + cb) {
-            uint32_t m = b;
-            for (uint32_t q = ex; q < rr; ++q) m &= m - 1u;  // drop the lower members
-            sh.result[t] = c * 8 + (__ffs(m) - 1);
+            for (uint32_t k = 0; k < n; ++k) {
+              const int id = static_cast<int>(hlist[t][k]);
+              if ((id >> 3) == c) b |= 1u << (id & 7);
+            }
+            const uint32_t cb = static_cast<uint32_t>(__popc(b));
+            const uint32_t ex = wave_incl_scan(cb) - cb;
+            if (ex <= rr && rr < ex + cb) {
+              uint32_t m = b;
+              for (uint32_t q = ex; q < rr; ++q) m &= m - 1u;  // drop the lower members
+              sh.result[t] = c * 8 + (__ffs(m) - 1);
+            }
           }
         }
       } else {
