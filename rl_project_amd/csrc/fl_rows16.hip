@@ -867,17 +867,23 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (!active[t]) continue;
-      const bool zero_in = in_range(t, 0u);
-      const bool pad_in = pad > 0 && zero_in;
+      const int zero_in = __builtin_amdgcn_readfirstlane(in_range(t, 0u) ? 1 : 0);
       if (fast) {
 #pragma unroll
         for (int j = 0; j < NCH; ++j) {
           const uint32_t w4[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
-          uint32_t m[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
+          uint32_t m[4];
+          {
+            const uint32_t lo2 = rlo[2 * t] * 0x10001u, wd2 = rw[2 * t] * 0x10001u;
 #pragma unroll
-          for (int rr = 2 * t; rr < 2 * t + 2; ++rr) {
-            if (!ren[rr]) continue;  // wave-uniform
-            const uint32_t lo2 = rlo[rr] * 0x10001u, wd2 = rw[rr] * 0x10001u;
+            for (int k = 0; k < 4; ++k)
+              asm("v_pk_sub_u16 %0, %1, %2\n\t"
+                  "v_pk_sub_u16 %0, %0, %3 clamp"
+                  : "=&v"(m[k])
+                  : "v"(w4[k]), "s"(lo2), "s"(wd2));
+          }
+          if (ren[2 * t + 1]) {  // wave-uniform: a range across zero has a second part
+            const uint32_t lo2 = rlo[2 * t + 1] * 0x10001u, wd2 = rw[2 * t + 1] * 0x10001u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
               uint32_t e;
@@ -893,20 +899,27 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
           asm("v_pk_min_u16 %0, %1, %2" : "=v"(mm) : "v"(m[0]), "v"(m[1]));
           asm("v_pk_min_u16 %0, %1, %2" : "=v"(m23) : "v"(m[2]), "v"(m[3]));
           asm("v_pk_min_u16 %0, %0, %1" : "+v"(mm) : "v"(m23));
-          const int c = j * NT + tid;
-          bool flag = ((mm & 0xFFFFu) == 0u) | (mm < 0x10000u);
-          // lanes past the row hold zeros, members only if +0.0 is a target
-          if (zero_in && (j + 1) * NT > nchunks) flag = flag && c < nchunks;
-          if (__ballot(flag) != 0ull) {  // wave-uniform
+          // (lanes past the row hold zeros: flagged only if +0.0 is a target)
+          if (__ballot(static_cast<uint16_t>(mm) == 0u || mm < 0x10000u) != 0ull) {  // wave-uniform
             uint32_t f0, f1, f2, f3;
             asm("v_pk_min_u16 %0, %1, %2" : "=v"(f0) : "v"(m[0]), "s"(ones2));
             asm("v_pk_min_u16 %0, %1, %2" : "=v"(f1) : "v"(m[1]), "s"(ones2));
             asm("v_pk_min_u16 %0, %1, %2" : "=v"(f2) : "v"(m[2]), "s"(ones2));
             asm("v_pk_min_u16 %0, %1, %2" : "=v"(f3) : "v"(m[3]), "s"(ones2));
             const uint32_t nm = f0 + f1 + f2 + f3;  // halves at most 4: no carry between them
-            uint32_t cj = flag ? 8u - ((nm & 0xFFFFu) + (nm >> 16)) : 0u;
-            if (pad_in && c == nfull) cj -= static_cast<uint32_t>(pad);
+            const uint32_t cj = 8u - ((nm & 0xFFFFu) + (nm >> 16));
             if (cj) atomicAdd(&sh.wc[t][j][wv], cj);
+          }
+        }
+        // +0.0 a target: take back the zeros of the padding and of the lanes
+        // past the row
+        if (zero_in && lane_id == 0) {
+#pragma unroll
+          for (int j = 0; j < NCH; ++j) {
+            const int c0 = j * NT + wv * WAVE;
+            uint32_t extra = 8u * static_cast<uint32_t>(min(WAVE, max(0, c0 + WAVE - nchunks)));
+            if (pad > 0 && nfull >= c0 && nfull < c0 + WAVE) extra += static_cast<uint32_t>(pad);
+            if (extra) atomicAdd(&sh.wc[t][j][wv], 0u - extra);
           }
         }
       } else {

@@ -165,3 +165,33 @@ def test_masked_vocabulary(dtype):
     # the float32 kernel on the same rows agrees on the all-masked status
     o32 = sample_tokens(x.cuda(), uniforms=w.uniforms.cuda(), check_status=False)
     assert int(o32.status.cpu()[4]) == FL_ROW_ALL_MASKED
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [50257, 4099, 32001])
+def test_last_element_of_odd_vocab(dtype, V):
+    """The largest logit at the last index of a row whose length is odd (its
+    last 16-byte chunk is partial): greedy, top-k 1 and a tie with an earlier
+    index must all find it where it is."""
+    import dataclasses
+    B = 3
+    print(f"[last element {dtype}] V={V}", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=31, batch=B, vocab=V)
+    g = torch.Generator().manual_seed(31)
+    x = 2.0 * torch.randn(B, V, generator=g)
+    x[:, V - 1] = 12.0
+    x[2, 7] = 12.0                      # row 2: a tie of the last index with index 7
+    w = dataclasses.replace(w, logits=x.to(dtype), history=None,
+                            temperature=torch.tensor([0.0, 0.7, 0.7]),
+                            top_k=torch.tensor([0, 1, 2], dtype=torch.int32),
+                            top_p=torch.ones(B), min_p=torch.zeros(B), repetition_penalty=torch.ones(B),
+                            uniforms=torch.tensor([0.5, 0.5, 0.75]))
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0
+    toks = out.tokens.cpu().tolist()
+    assert toks[0] == V - 1 and toks[1] == V - 1, toks
+    assert toks[2] == V - 1, toks          # u = 0.75 of two equal members: the second in index order
+    assert bool(keep[0, V - 1]) and bool(keep[2, 7]) and bool(keep[2, V - 1])
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
