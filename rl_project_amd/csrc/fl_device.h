@@ -292,6 +292,13 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_
   tb = sb;
 }
 
+// Lane l's value of a 64-bit quantity (l wave-uniform).
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // First index i in [a, b) with pred(i) true, for a predicate that is false
 // then true along the range (b if it never holds).  The 64 lanes of a wave
 // probe 64 evenly spaced indices per step, so a range of n needs about

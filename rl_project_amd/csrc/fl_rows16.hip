@@ -75,12 +75,6 @@ struct ScanHit {
   uint64_t total;  // sum of all terms (or the total passed in)
 };
 
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 // Block-wide search along n terms in index order: the first i for which
 // pred(i, excl_i, total) holds, excl_i being the sum of the terms before i
 // (the predicate must be false, then true, along the indices).  The terms are

@@ -93,7 +93,7 @@ __device__ __forceinline__ float prob_of(const fl_row_desc& ds, float y, int64_t
 constexpr int MAX_ROUNDS = 64;
 // Sliced residual: at most this many slices of a row pair per sequence, and
 // this many threads per slice work-group.
-constexpr int MAX_SLICES = 16;
+constexpr int MAX_SLICES = WAVE;  // slices of a row pair (one per lane of a wave in the pick)
 constexpr int NT_PART = 256;
 
 struct SharedSpec {
@@ -327,7 +327,7 @@ __device__ __forceinline__ void write_tail(const fl_spec_args& a, int64_t b, int
 
 // Slices of a row pair for the sliced residual path.
 __host__ __device__ inline int spec_slices(int64_t batch) {
-  int64_t s = batch > 0 ? 512 / batch : 1;
+  int64_t s = batch > 0 ? 2048 / batch : 1;
   return static_cast<int>(s < 1 ? 1 : (s > MAX_SLICES ? MAX_SLICES : s));
 }
 
@@ -413,8 +413,9 @@ __global__ __launch_bounds__(NT_PART) void k_spec_part(const fl_spec_args a, Spe
   if constexpr (!PASS2) {
     v = range_sum(R, c0, c1, NT_PART, [](float p, float q) { return resid_of<D>(p, q); });
   } else {
-    uint64_t rsum = 0;
-    for (int j = 0; j < ws.S; ++j) rsum += ws.part1[b * ws.S + j];
+    // sum(r) over the slices: one slice per lane, in every wave
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint64_t rsum = wave_reduce(lane < ws.S ? ws.part1[b * ws.S + lane] : 0ull, OpAdd());
     const Weight<D> wt(rsum);
     v = range_sum(R, c0, c1, NT_PART, wt);
   }
@@ -430,17 +431,20 @@ __global__ __launch_bounds__(NT) void k_spec_pick(const fl_spec_args a, SpecWs w
   const int pos = ws.state[b];
   if (pos < 0) return;
   const PairRows<D> R(a, b, pos);
-  uint64_t rsum = 0, W = 0;
-  for (int j = 0; j < ws.S; ++j) {
-    rsum += ws.part1[b * ws.S + j];
-    W += ws.part2[b * ws.S + j];
-  }
+  // one slice per lane, in every wave: the totals, then the first slice
+  // whose inclusive weight exceeds the target (the last slice if none does)
+  const int lane = threadIdx.x & (WAVE - 1);
+  const uint64_t p1 = lane < ws.S ? ws.part1[b * ws.S + lane] : 0ull;
+  const uint64_t p2 = lane < ws.S ? ws.part2[b * ws.S + lane] : 0ull;
+  const uint64_t rsum = wave_reduce(p1, OpAdd());
+  const uint64_t inc = wave_incl_scan(p2);
+  const uint64_t W = readlane64(inc, WAVE - 1);
   const Weight<D> wt(rsum);
   const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
   const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(U) * static_cast<double>(W)));
-  int s = 0;
-  uint64_t base = 0;
-  while (s < ws.S - 1 && base + ws.part2[b * ws.S + s] <= target) base += ws.part2[b * ws.S + s++];
+  const uint64_t hit = __ballot(lane < ws.S - 1 && inc > target);
+  const int s = hit ? __ffsll(static_cast<unsigned long long>(hit)) - 1 : ws.S - 1;
+  const uint64_t base = readlane64(inc - p2, s);
   const int cps = (R.nch + ws.S - 1) / ws.S;
   const int c0 = min(R.nch, s * cps), c1 = min(R.nch, c0 + cps);
   const int t = pick_in_range(sh, R, wt, c0, c1, false, U, base, target);

@@ -150,8 +150,10 @@ def test_spec_workspace_bytes_and_checks():
     L = _lib.lib()
     n = ctypes.c_size_t(0)
     assert L.fl_spec_workspace_bytes(32, ctypes.byref(n)) == _lib.FL_OK
-    # int32 state per sequence (padded to 8 bytes), two uint64 slice sums per slice (16 slices at 32 sequences)
-    assert n.value == 128 + 2 * 8 * 32 * 16
+    # int32 state per sequence (padded to 8 bytes), two uint64 slice sums per slice (64 slices at 32 sequences)
+    assert n.value == 128 + 2 * 8 * 32 * 64
+    assert L.fl_spec_workspace_bytes(512, ctypes.byref(n)) == _lib.FL_OK
+    assert n.value == 2048 + 2 * 8 * 512 * 4     # 4 slices at 512 sequences
     assert L.fl_spec_workspace_bytes(-1, ctypes.byref(n)) == _lib.FL_EINVAL
     assert L.fl_spec_workspace_bytes(4, None) == _lib.FL_EINVAL
     s = _lib.SpecArgs()
