@@ -257,8 +257,10 @@ __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
 }
 
 // Exclusive prefix sums of two quantities in thread order with one pair of
-// barriers; ta / tb receive the totals.
-template <int NW = NWAVE>
+// barriers; ta / tb receive the totals.  TRAIL false leaves out the second
+// barrier, for callers that pass a barrier of their own before ra / rb are
+// written again.
+template <int NW = NWAVE, bool TRAIL = true>
 __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_t* ra, uint64_t* rb, uint32_t& ea,
                                                  uint64_t& eb, uint32_t& ta, uint64_t& tb) {
   const int lane = threadIdx.x & (WAVE - 1);
@@ -285,7 +287,7 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint64_t b, uint32_
     sa += x;
     sb += y;
   }
-  __syncthreads();
+  if constexpr (TRAIL) __syncthreads();
   ea = ba + xa;
   eb = bb + xb;
   ta = sa;

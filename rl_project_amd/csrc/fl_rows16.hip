@@ -524,7 +524,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     uint32_t ec, tc;
     uint64_t em, tm;
-    block_excl_scan2(lc, lm, sh.redu, sh.redq, ec, em, tc, tm);
+    // (no trailing barrier: sh.redu / sh.redq are next written after the
+    // decisions' barriers)
+    block_excl_scan2<NWAVE, false>(lc, lm, sh.redu, sh.redq, ec, em, tc, tm);
     SliceCnt[tid] = ec;
     SliceM[tid] = em;
     if (cached) {
