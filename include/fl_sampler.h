@@ -58,7 +58,7 @@ enum fl_row_status {
 
 /* Limits of this build. */
 #define FL_MAX_VOCAB_F32 262144     /* fp32 rows                       */
-#define FL_MAX_VOCAB_16  131072     /* bf16 / fp16 rows                */
+#define FL_MAX_VOCAB_16  262144     /* bf16 / fp16 rows (repetition penalty: 131072) */
 #define FL_MAX_HISTORY   65536      /* history ids per row             */
 
 /*

@@ -22,7 +22,7 @@ FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
 FL_FLAG_NO_SELECT = 1
 FL_MAX_VOCAB_F32 = 262144
-FL_MAX_VOCAB_16 = 131072
+FL_MAX_VOCAB_16 = 262144
 FL_MAX_HISTORY = 65536
 
 ROW_STATUS_NAMES = {

@@ -29,7 +29,9 @@ namespace {
 
 constexpr int NCH = 16;                          // 16-byte chunks per thread
 constexpr int HIST_WORDS = 32768;                // 65536 packed u16 counters
-constexpr int HBITS_WORDS = FL_MAX_VOCAB_16 / 32;
+constexpr int TILE_V = NCH * NT * 8;              // the VGPR tile: rows up to this length stay in registers
+constexpr int HBITS_WORDS = TILE_V / 32;          // history bitmap (penalty rows up to TILE_V values)
+constexpr int NSLOT = FL_MAX_VOCAB_16 / (NT * 8);  // identification slots of NT chunks
 constexpr int OWNER_WORDS = FL_MAX_HISTORY / 32;
 constexpr int HLIST_CAP = HIST_WORDS / 8;         // history members listed per identification target
 constexpr int SLICE_BASE = HIST_WORDS - 3 * NT;   // slice tables: count u32[NT], mass u64[NT]
@@ -40,7 +42,7 @@ constexpr int SPW = NSTEP / NWAVE;                // steps per wave
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 constexpr int EARLY_CHUNKS = 2;                  // row chunks per thread requested before the LDS clear
 
-static_assert(NCH * NT * 8 == FL_MAX_VOCAB_16, "one VGPR tile holds the largest 16-bit row");
+static_assert(NSLOT * NT * 8 == FL_MAX_VOCAB_16 && NSLOT >= NCH, "identification slots cover the longest row");
 
 struct Shared16 {
   uint32_t hist[HIST_WORDS + WAVE];  // pattern counts, then one -inf counter per lane
@@ -61,7 +63,7 @@ struct Shared16 {
     uint32_t o_lo[2], o_hi[2];
     float y_sel, y_cut;
   } dec;  // results of the search wave
-  uint32_t wc[2][NCH][NWAVE];  // identification: members per slot of NT chunks and wave
+  uint32_t wc[2][NSLOT][NWAVE];  // identification: members per slot of NT chunks and wave
   uint32_t nh[2];         // identification: history members
 };
 
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const uint16_t* row = static_cast<const uint16_t*>(a.logits) + b * a.ld;
   const bool SC_ELEM = SC && SC_ELEM_IN;
   const int nfull = V >> 3;                               // chunks holding 8 valid elements
-  const bool fast = ALIGNED && !SC_ELEM && nfull > 0;     // whole row through the VGPR tile
+  const bool fast = ALIGNED && !SC_ELEM && nfull > 0 && V <= TILE_V;  // whole row through the VGPR tile
 
   // ------------------------------------------------ loads
   // Issue order matters: the per-row parameters (scalar loads) first, so they
@@ -242,8 +244,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   if (tid < WAVE) sh.hist[HIST_WORDS + tid] = 0;
   reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
   if (tid < OWNER_WORDS / 4) reinterpret_cast<uint4*>(sh.owner)[tid] = make_uint4(0, 0, 0, 0);
-  static_assert(2 * NCH * NWAVE <= NT, "one member counter per thread to clear");
-  if (tid < 2 * NCH * NWAVE) (&sh.wc[0][0][0])[tid] = 0;
+  static_assert(2 * NSLOT * NWAVE <= NT, "one member counter per thread to clear");
+  if (tid < 2 * NSLOT * NWAVE) (&sh.wc[0][0][0])[tid] = 0;
   if (tid == 0) {
     sh.status = 0;
     sh.nh[0] = sh.nh[1] = 0;
@@ -280,10 +282,12 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const float CAP = a.softcap;
   // (H_in is only meaningful with a history: without one it was read from the stand-in array)
   const bool hist_too_long = a.hist_ids != nullptr && H_in > FL_MAX_HISTORY;
-  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
+  // (the history bitmap covers TILE_V values: a longer row is penalised nowhere)
+  const bool pen_too_wide = a.hist_ids != nullptr && RP != 1.0f && H_in > 0 && V > TILE_V;
+  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long && !pen_too_wide) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
   const bool sc_entry = SC && (CAP > 0.0f) && !SC_ELEM;
-  if (tid == 0 && hist_too_long) atomicOr(&sh.status, FL_ROW_LIMIT);
+  if (tid == 0 && (hist_too_long || pen_too_wide)) atomicOr(&sh.status, FL_ROW_LIMIT);
 
   // Value pattern of an element as the filters see it before penalty.
   auto elem_bits = [&](uint32_t raw) -> uint32_t {
@@ -919,7 +923,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
           }
         }
       } else {
-        for (int j = 0; j < NCH; ++j) {
+        for (int j = 0; j < NSLOT; ++j) {
           const int c = j * NT + tid;
           if (c >= nchunks) break;
           const uint32_t cj = static_cast<uint32_t>(__popc(chunk_mask(t, c, load_chunk16(row, c, V, ALIGNED))));
@@ -960,27 +964,36 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       const uint32_t n = sh.nh[t];
       if (n <= static_cast<uint32_t>(HLIST_CAP)) {
         // The (slot, wave) holding rank r, found by every wave alike: lane l
-        // reads the counts of slot l / 4, waves 4 (l % 4) .. + 3, which puts
-        // the lanes in index order; an inclusive scan over the lanes finds
-        // the lane, four compares the wave.  That wave alone then forms its
-        // lanes' members in the slot (the chunk's non-history members and
-        // the listed history members in the chunk) and scans them.
-        static_assert(NCH * NWAVE == 4 * WAVE, "four counters per lane");
-        const uint4 q4 = reinterpret_cast<const uint4*>(&sh.wc[t][0][0])[lane_id];
-        const uint32_t s4 = q4.x + q4.y + q4.z + q4.w;
-        const uint32_t inc = wave_incl_scan(s4);
-        const uint64_t hit = __ballot(inc > rank[t]);
-        if (hit != 0ull) {  // the same in every wave
+        // reads the counts of slot l / 4, waves 4 (l % 4) .. + 3 (16 slots a
+        // round, the second round only for rows past TILE_V), which puts the
+        // lanes in index order; an inclusive scan over the lanes finds the
+        // lane, four compares the wave.  That wave alone then forms its
+        // lanes' members in the slot (the chunk's non-history members and the
+        // listed history members in the chunk) and scans them.
+        static_assert(NCH * NWAVE == 4 * WAVE && NSLOT % NCH == 0, "four counters per lane, NCH slots a round");
+        int ws = -1, js = 0;
+        uint32_t rr = rank[t];
+        for (int j0 = 0; j0 < NSLOT && ws < 0 && j0 * NT * 8 < V; j0 += NCH) {
+          const uint4 q4 = reinterpret_cast<const uint4*>(&sh.wc[t][j0][0])[lane_id];
+          const uint32_t s4 = q4.x + q4.y + q4.z + q4.w;
+          const uint32_t inc = wave_incl_scan(s4);
+          const uint64_t hit = __ballot(inc > rr);
+          if (hit == 0ull) {  // the same in every wave
+            rr -= static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inc), WAVE - 1));
+            continue;
+          }
           const int L = __ffsll(static_cast<unsigned long long>(hit)) - 1;
-          uint32_t rr = rank[t] - static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inc - s4), L));
+          rr -= static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inc - s4), L));
           const uint32_t qc[4] = {static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.x), L)),
                                   static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.y), L)),
                                   static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.z), L)),
                                   static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(q4.w), L))};
           int kq = 0;
           while (kq < 3 && rr >= qc[kq]) rr -= qc[kq++];
-          const int ws = 4 * (L & 3) + kq;
-          const int js = L >> 2;
+          ws = 4 * (L & 3) + kq;
+          js = j0 + (L >> 2);
+        }
+        {
           if (wv == ws) {
             const int c = js * NT + tid;
             uint32_t b = 0;
@@ -1012,7 +1025,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         // the history member list overflowed: count members round by round
         // in index order (re-reads the row from memory; a rare path)
         uint32_t base = 0;
-        for (int j = 0; j < NCH; ++j) {
+        for (int j = 0; j < NSLOT && j * NT * 8 < V; ++j) {
           const int e0 = (j * NT + tid) * 8;
           uint32_t m = 0;
           for (int e = 0; e < 8; ++e) {
