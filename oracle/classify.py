@@ -130,11 +130,22 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 C = np.cumsum(ps)
                 t = float(_rn(np.float64(p.top_p), dt))
                 pos = np.nonzero(np.isin(order.numpy(), grp))[0]
+                # Probabilities whose rounding to the dtype is itself open
+                # (the exact value sits at a rounding midpoint of the dtype,
+                # closer than the reference's float32 softmax error) may come
+                # out one unit apart on the two sides; a whole group of them
+                # moves the cumulative sums after it by that group's size in
+                # units.  The softmax denominator's float32 summation error
+                # grows with the row length: about sqrt(V) units of 2^-24.
+                rel_p = max(rel, 2.0 * np.sqrt(float(V)) * 2.0 ** -24)
+                p64 = F.softmax(srt.double(), dim=-1).numpy()
+                amb = np.abs(_rn(p64 * (1.0 + rel_p), dt) - _rn(p64 * (1.0 - rel_p), dt))
+                U = np.cumsum(amb) - amb
 
                 def removed(c, pp):
                     return bool(_rn(_rn(c, dt) - pp, dt) >= t)
                 for j in pos:
-                    if _perturbed(removed, [C[j], ps[j]], rel):
+                    if _perturbed(removed, [C[j], ps[j]], rel) or removed(C[j] - U[j], ps[j]) != removed(C[j] + U[j], ps[j]):
                         explained = True
                         margins.append(abs(C[j] - ps[j] - p.top_p) / max(p.top_p, 1e-30))
                         verdict.details.append(f"near top-p y={v:.9g} excl={C[j] - ps[j]:.9g} top_p={p.top_p}")
