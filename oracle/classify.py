@@ -115,11 +115,16 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 S = S[np.isfinite(pre_minp[0].double().numpy())].sum()
                 r = 1.0 / S
 
+                mp = np.float32(p.min_p)  # torch multiplies by the Python scalar in float32
+
                 def keep_minp(e_, r_):
-                    return _rn(e_ * r_, dt) >= _rn(_rn(r_, dt) * np.float32(p.min_p), dt)
-                if _perturbed(lambda a, b: bool(keep_minp(a, b)), [e, r], rel):
+                    return _rn(e_ * r_, dt) >= _rn(_rn(r_, dt) * mp, dt)
+                # the same test on the oracle's own softmax output, whose
+                # rounding may differ from the exact value's by one unit
+                keep_or = bool(probs[grp[0]] >= _rn(probs.max() * mp, dt))
+                if _perturbed(lambda a, b: bool(keep_minp(a, b)), [e, r], rel) or keep_or != bool(keep_minp(e, r)):
                     explained = True
-                    margins.append(abs(e * r - float(_rn(_rn(r, dt) * np.float32(p.min_p), dt))) / (e * r))
+                    margins.append(abs(e * r - float(_rn(_rn(r, dt) * mp, dt))) / (e * r))
                     verdict.details.append(f"near min-p y={v:.9g}")
                 del probs
             # top-p boundary
@@ -130,17 +135,23 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 C = np.cumsum(ps)
                 t = float(_rn(np.float64(p.top_p), dt))
                 pos = np.nonzero(np.isin(order.numpy(), grp))[0]
-                # Probabilities whose rounding to the dtype is itself open
-                # (the exact value sits at a rounding midpoint of the dtype,
-                # closer than the reference's float32 softmax error) may come
-                # out one unit apart on the two sides; a whole group of them
-                # moves the cumulative sums after it by that group's size in
-                # units.  The softmax denominator's float32 summation error
-                # grows with the row length: about sqrt(V) units of 2^-24.
-                rel_p = max(rel, 2.0 * np.sqrt(float(V)) * 2.0 ** -24)
+                # A probability may come out one unit of the dtype apart on
+                # the two sides: where the oracle's own softmax rounds away from
+                # the correctly rounded value (torch's vectorised float32
+                # softmax on the CPU is up to ~5e-5 relative off), or where the
+                # exact value sits within `rel` of a rounding midpoint.  A
+                # whole group of such members moves the cumulative sums after
+                # it by the group's size in units.
                 p64 = F.softmax(srt.double(), dim=-1).numpy()
-                amb = np.abs(_rn(p64 * (1.0 + rel_p), dt) - _rn(p64 * (1.0 - rel_p), dt))
-                U = np.cumsum(amb) - amb
+                amb = np.maximum(np.abs(_rn(p64 * (1.0 + rel), dt) - _rn(p64 * (1.0 - rel), dt)),
+                                 np.abs(ps - _rn(p64, dt)))
+                # for 16-bit rows the reference accumulates the cumulative sums
+                # sequentially in float32 (float32 rows: in float64); the
+                # drift from the exact sums adds to the doubt
+                drift = 0.0
+                if dt != torch.float32:
+                    drift = np.abs(np.cumsum(ps.astype(np.float32), dtype=np.float32).astype(np.float64) - C)
+                U = np.cumsum(amb) - amb + drift
 
                 def removed(c, pp):
                     return bool(_rn(_rn(c, dt) - pp, dt) >= t)

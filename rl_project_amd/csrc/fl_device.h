@@ -65,7 +65,13 @@ struct F16 {
   __device__ static __forceinline__ float to_f32(uint32_t b) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(b)));
   }
-  __device__ static __forceinline__ uint32_t from_f32(float x) { return __half_as_ushort(__float2half_rn(x)); }
+  // (the empty asm keeps x a rounded float32: without it the compiler fuses
+  // a product into this conversion (v_fma_mixlo_f16) and rounds the exact
+  // product once, where the reference rounds it to float32 first)
+  __device__ static __forceinline__ uint32_t from_f32(float x) {
+    asm("" : "+v"(x));
+    return __half_as_ushort(__float2half_rn(x));
+  }
   __device__ static __forceinline__ float rn(float x) { return to_f32(from_f32(x)); }
 };
 
@@ -124,22 +130,24 @@ __device__ __forceinline__ float temperature_val(float x, float t) {
 }
 
 // ------------------------------------------------- fixed-point masses
-// Probabilities in [0, 1] as unsigned 2^-46 fixed point: sums are exact and
-// associative (deterministic scans), and stay below 2^53 so that converting a
-// sum back to double is exact.
-constexpr double FX_ONE = 70368744177664.0;  // 2^46
-// round(p * 2^46) for p in [0, 1] from the float's fields (ties round up);
+// Masses e in [0, 1] as unsigned 2^-45 fixed point: sums are exact and
+// associative (deterministic scans), and a row of up to 2^18 values sums to
+// below 2^63 even when every e is 1 (probabilities, which sum to 1, stay
+// below 2^53, so converting their sums back to double is exact).
+constexpr int FX_BITS = 45;
+constexpr double FX_ONE = 35184372088832.0;  // 2^45
+// round(p * 2^45) for p in [0, 1] from the float's fields (ties round up);
 // integer arithmetic only
-// (branch-free: with m = the 24-bit significand, p * 2^46 = m * 2^(ex - 104)
-// = (m << 24) >> (128 - ex); a right shift of 49 or more leaves 0, as do
+// (with m = the 24-bit significand, p * 2^45 = m * 2^(ex - 105)
+// = (m << 24) >> (129 - ex); a right shift of 49 or more leaves 0, as do
 // zero and denormals)
 __device__ __forceinline__ uint64_t to_fx(float p) {
   const uint32_t u = __float_as_uint(p);
   const uint32_t ex = u >> 23;
   const uint64_t m24 = static_cast<uint64_t>((u & 0x7FFFFFu) | 0x800000u) << 24;
-  const uint32_t sh = min(128u - ex, 63u);  // ex <= 127 for p <= 1 (p > 1 handled below)
+  const uint32_t sh = min(129u - ex, 63u);  // ex <= 127 for p <= 1 (p > 1 handled below)
   const uint64_t r = (m24 + (1ull << (sh - 1))) >> sh;
-  return ex > 127u ? (m24 >> 24) << min(ex - 104u, 63u) : r;
+  return ex > 128u ? (m24 >> 24) << min(ex - 105u, 63u) : r;
 }
 __device__ __forceinline__ double from_fx(uint64_t v) { return static_cast<double>(v) * (1.0 / FX_ONE); }
 

@@ -720,7 +720,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     } else {
       // inverse CDF (CONVENTION replacing torch.multinomial, sampling.py:61):
       // first member whose inclusive cumulative probability exceeds u * total,
-      // cumulative sums in exact 2^-46 fixed point
+      // cumulative sums in exact 2^-45 fixed point
       auto qf = [&](int i) -> uint64_t { return to_fx(D::rn(E(i) * rK)); };
       const int n = i0 + 1;
       uint64_t Q = 0;

@@ -228,3 +228,76 @@ def test_rows_longer_than_the_register_tile(dtype, V):
     o2 = sample_tokens(wp.logits, check_status=False, **wp.kwargs())
     st = o2.status.cpu().tolist()
     assert st[1] == FL_ROW_LIMIT and all(s == 0 for i, s in enumerate(st) if i != 1), st
+
+
+def test_long_row_of_near_equal_values():
+    """262144 bf16 values all within 1e-3 of each other: every exp(y - M) is
+    about 1, so the fixed-point mass of the row is about 2^18 units of one,
+    the most a 64-bit sum has to hold."""
+    import dataclasses
+    B, V = 2, 262144
+    print(f"[near-equal long rows] B={B} V={V}", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=43, batch=B, vocab=V)
+    g = torch.Generator().manual_seed(43)
+    x = (1e-3 * torch.randn(B, V, generator=g)).to(torch.bfloat16)
+    w = dataclasses.replace(w, logits=x, history=None, repetition_penalty=torch.ones(B),
+                            temperature=torch.tensor([1.0, 0.7]), top_k=torch.zeros(B, dtype=torch.int32),
+                            top_p=torch.tensor([0.5, 1.0]), min_p=torch.zeros(B))
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0, status.tolist()
+    n_keep = keep.sum(1).tolist()
+    assert 100000 < n_keep[0] < 160000 and n_keep[1] == V, n_keep
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
+
+
+def _sweep_row(seed: int, row: int):
+    """Row ``row`` of case ``seed`` of a randomized parity sweep (logits, row
+    parameters, history ids, soft-cap), rebuilt from its two seeded streams."""
+    import random
+    rng = random.Random(seed)
+    dt = rng.choice([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
+    V = rng.choice([7, 100, 1000, 4099, 32000, 50257, 128256, 151936])
+    B = rng.choice([1, 3, 8, 16])
+    g = torch.Generator().manual_seed(seed)
+    kind = rng.choice(["normal", "grid", "wide", "masked", "peaked"])
+    scale = rng.choice([0.5, 1.0, 2.5, 6.0])
+    x = scale * torch.randn(B, V, generator=g)
+    assert kind == "normal"
+    T = [rng.choice([0.0, 0.1, 0.7, 1.0, 1.5]) for _ in range(B)]
+    K = [rng.choice([0, 1, 5, 50, 1000]) for _ in range(B)]
+    P = [rng.choice([1.0, 0.5, 0.9, 0.99]) for _ in range(B)]
+    MP = [rng.choice([0.0, 0.0, 0.05, 0.3]) for _ in range(B)]
+    RP = [rng.choice([1.0, 1.2, 0.8]) for _ in range(B)]
+    H = rng.choice([0, 8, 300])
+    hist = torch.randint(0, V, (B, H), generator=g, dtype=torch.int32) if H else None
+    if hist is not None and rng.random() < 0.5:
+        hist[:, H // 2:] = -1
+    softcap = rng.choice([0.0, 0.0, 30.0, 5.0])
+    h = None if hist is None else hist[row:row + 1]
+    return (x[row:row + 1].to(dt), T[row], K[row], P[row], MP[row], RP[row], h, softcap)
+
+
+def test_f16_product_rounds_through_float32():
+    """A float16 row whose min-p threshold, min_p * max(p) in float32, lies
+    exactly halfway between two float16 values (max(p) = 1.0311603546142578e-04,
+    min_p 0.05): the reference rounds the float32 product to even and keeps
+    the 22 elements at the lower value; a product fused into the float16
+    conversion rounds once, up, and drops them."""
+    import dataclasses
+    x, T, K, P, MP, RP, h, softcap = _sweep_row(902, 8)
+    assert x.dtype == torch.float16 and MP == 0.05 and K == 0 and P == 1.0
+    w = workloads.make("hetero_bf16_256x128256", seed=902, batch=1, vocab=x.size(1))
+    w = dataclasses.replace(w, logits=x, history=h, temperature=torch.tensor([T]),
+                            top_k=torch.tensor([K], dtype=torch.int32), top_p=torch.tensor([P]),
+                            min_p=torch.tensor([MP]), repetition_penalty=torch.tensor([RP]), softcap=softcap)
+    if h is not None:
+        w = dataclasses.replace(w, history=h[:, : int((h >= 0).sum())])
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]

@@ -382,3 +382,20 @@ def test_rowstats_oracle_ignore_index_and_neg_inf():
     assert float(lp[0]) == 0.0 and str(float(lp[0])) == "-0.0"
     assert torch.isnan(L.entropy_from_logits(x)).all()
     assert torch.isfinite(L.token_logprobs_from_logits(x, torch.tensor([2]))).all()
+
+
+def test_scalar_products_of_16_bit_tensors_use_float32_scalars():
+    """``min_p * probs.max()`` (sampling.py:42) on a 16-bit tensor multiplies
+    by the Python scalar in float32 and rounds the product once, whereas a
+    comparison with a scalar (``>= top_p``) takes the scalar in the tensor's
+    dtype; the kernels follow both."""
+    g = torch.Generator().manual_seed(0)
+    for dt in (torch.bfloat16, torch.float16):
+        x = (torch.rand(4096, generator=g) * 2).to(dt)
+        for s in (0.05, 0.1, 0.3):
+            as_f32 = (torch.tensor(s, dtype=torch.float32) * x.float()).to(dt)
+            as_dt = (torch.tensor(s).to(dt).float() * x.float()).to(dt)
+            assert torch.equal(s * x, as_f32)
+            assert not torch.equal(as_f32, as_dt)   # the two readings do differ
+    b = torch.tensor([0.94921875, 0.953125], dtype=torch.bfloat16)
+    assert (b >= 0.95).tolist() == [True, True]     # 0.95 compares as bf16 0.94921875
