@@ -65,6 +65,7 @@ struct Shared16 {
   } dec;  // results of the search wave
   uint32_t wc[2][NSLOT][NWAVE];  // identification: members per slot of NT chunks and wave
   uint32_t nh[2];         // identification: history members
+  uint32_t inf_extra;     // soft-capped rows: -inf values beyond their pattern's 16-bit count
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -319,15 +320,23 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
 
   // ------------------------------------------------ count patterns
-  // -inf values (a masked vocabulary) are never kept, selected or weighted:
-  // they stay out of the pattern counts, where more than 65535 of them would
-  // wrap a 16-bit counter, and go to a 32-bit counter of this lane past the
-  // patterns (the -inf pattern is even, so its increment is 1).  With a
-  // per-entry soft-cap a raw -inf becomes -cap and is counted by its pattern.
-  const uint32_t neg_inf_bits = sc_entry ? 0xFFFFFFFFu : (0x8000u | D::INF_BITS);
+  // Raw -inf values (a masked vocabulary) stay out of the pattern counts,
+  // where more than 65535 of them would wrap a 16-bit counter, and go to a
+  // 32-bit counter of this lane past the patterns.  Without a soft-cap they
+  // are never kept, selected or weighted.  With one they are the value -cap:
+  // after the counting they join their pattern's count, the part beyond 16
+  // bits kept apart (inf_extra).
+  constexpr uint32_t NEG_INF_RAW = 0x8000u | D::INF_BITS;
   const uint32_t inf_word = HIST_WORDS + (tid & (WAVE - 1));
-  auto count = [&](uint32_t bits) {
-    atomicAdd(&sh.hist[bits == neg_inf_bits ? inf_word : bits >> 1], 1u + (bits & 1u) * 0xFFFFu);
+  auto count = [&](uint32_t raw) {
+    if constexpr (SC) {
+      const uint32_t bits = elem_bits(raw);
+      const bool ni = raw == NEG_INF_RAW;
+      atomicAdd(&sh.hist[ni ? inf_word : bits >> 1], ni ? 1u : 1u + (bits & 1u) * 0xFFFFu);
+    } else {
+      // (the -inf pattern is even, so its increment is 1)
+      atomicAdd(&sh.hist[raw == NEG_INF_RAW ? inf_word : raw >> 1], 1u + (raw & 1u) * 0xFFFFu);
+    }
   };
   if (fast) {
 #pragma unroll
@@ -343,11 +352,11 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       const uint4 q = load_chunk16(row, c, V, ALIGNED);
       const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) count(elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu));
+      for (int e = 0; e < 8; ++e) count((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
     }
   }
   if (tid == 0)
-    for (int i = nfull * 8; i < V; ++i) count(elem_bits(row[i]));
+    for (int i = nfull * 8; i < V; ++i) count(row[i]);
 
   FL_MARK(12);
   // ------------------------------------------------ repetition penalty
@@ -356,7 +365,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     const uint32_t z = elem_bits(raw);
     const uint32_t zp = penalised_bits<D>(z, RP);
     if (zp != z) {
-      atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
+      // (a soft-capped raw -inf was counted in this lane's -inf counter)
+      if (SC && raw == NEG_INF_RAW) atomicAdd(&sh.hist[inf_word], 0xFFFFFFFFu);
+      else atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
       atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
     }
   };
@@ -368,6 +379,28 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     if (claim(i, id)) penalise(row[id]);
   }
   __syncthreads();
+  // soft-capped rows: the -inf values join the count of their pattern (that of
+  // -cap), as far as its 16 bits hold
+  uint32_t inf_extra = 0, inf_order = 0xFFFFFFFFu;
+  if constexpr (SC) {
+    if (tid < WAVE) {
+      const uint32_t nin = wave_reduce(sh.hist[HIST_WORDS + tid], OpAdd{});
+      if (tid == 0) {
+        uint32_t add = 0;
+        if (nin != 0u) {
+          const uint32_t P = elem_bits(NEG_INF_RAW);
+          const uint32_t w = sh.hist[P >> 1];
+          const uint32_t cur = (P & 1u) ? (w >> 16) : (w & 0xFFFFu);
+          add = min(nin, 0xFFFFu - cur);
+          sh.hist[P >> 1] = w + ((P & 1u) ? (add << 16) : add);
+        }
+        sh.inf_extra = nin - add;
+      }
+    }
+    __syncthreads();
+    inf_extra = sh.inf_extra;
+    inf_order = order16(elem_bits(NEG_INF_RAW));
+  }
   FL_MARK(2);
 
   // ------------------------------------------------ compact to entries
@@ -483,6 +516,12 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // recomputed and prefixes are a slice-table read plus fewer than `per`
   // terms.
   uint32_t* ent = sh.hist;
+  // an entry's count: its 16 bits, and for the -cap entry of a soft-capped
+  // row the -inf values beyond them
+  auto entry_count = [&](uint32_t en) -> uint32_t {
+    if constexpr (SC) return (en & 0xFFFFu) + ((en >> 16) == inf_order ? inf_extra : 0u);
+    else return en & 0xFFFFu;
+  };
   const bool cached = N <= CACHE_MAX;
   float* Yc = reinterpret_cast<float*>(sh.hist + N);
   float* Ec = reinterpret_cast<float*>(sh.hist + 2 * N);
@@ -493,7 +532,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const int per = max(1, (N + NT - 1) / NT);
   const int lo = min(N, tid * per), hi = min(N, lo + per);
 
-  auto cnt_of = [&](int i) -> uint32_t { return ent[i] & 0xFFFFu; };
+  auto cnt_of = [&](int i) -> uint32_t { return entry_count(ent[i]); };
   auto y_raw = [&](int i) -> float { return y_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry); };
   const float M = N > 0 ? y_raw(0) : 0.0f;
   // -inf values of the row (read where a total is off or nothing is left)
@@ -522,7 +561,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
         Cc[i] = lc;  // prefix within the slice; the slice base is added below
         Cm[i] = lm;
       }
-      const uint32_t c = en & 0xFFFFu;
+      const uint32_t c = entry_count(en);
       lc += c;
       lm += c * to_fx(e);
     }

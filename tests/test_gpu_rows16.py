@@ -301,3 +301,37 @@ def test_f16_product_rounds_through_float32():
     print(summ)
     bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
     assert not bad, bad[:4]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_masked_vocabulary_with_softcap(dtype):
+    """Soft-capped rows with most of the vocabulary at -inf: the soft-cap
+    turns every -inf into -cap, a value that takes part in the softmax, so
+    more than 65535 equal values must be counted exactly (with and without a
+    repetition penalty; a row masked throughout becomes uniform)."""
+    import dataclasses
+    B, V = 4, 128256
+    print(f"[masked vocabulary, soft-cap {dtype}] B={B} V={V}", flush=True)
+    w = workloads.make("hetero_bf16_256x128256", seed=47, batch=B, vocab=V)
+    g = torch.Generator().manual_seed(47)
+    x = 2.5 * torch.randn(B, V, generator=g)
+    x[0, :100000] = float("-inf")
+    x[1, 3:] = float("-inf")            # three finite values and 128253 at -cap
+    x[2, :] = float("-inf")             # nothing but -cap: uniform
+    x[3, ::2] = float("-inf")
+    hist = w.history.clone()
+    hist[1, :4] = torch.tensor([0, 1, 500, 70000], dtype=hist.dtype)  # penalised ids, two of them masked
+    w = dataclasses.replace(w, logits=x.to(dtype), history=hist, softcap=3.0,
+                            temperature=torch.tensor([1.0, 0.8, 1.0, 1.2]),
+                            top_k=torch.tensor([0, 0, 0, 50], dtype=torch.int32),
+                            top_p=torch.tensor([1.0, 0.999, 1.0, 0.9]),
+                            min_p=torch.zeros(B),
+                            repetition_penalty=torch.tensor([1.0, 1.3, 1.0, 1.0]),
+                            uniforms=torch.tensor([0.3, 0.9, 0.123456, 0.5]))
+    out, keep, status = _run(w)
+    assert int(status.abs().sum()) == 0, status.tolist()
+    assert int(keep[2].sum()) == V
+    summ, verdicts = classify_workload(w, out.tokens, keep)
+    print(summ)
+    bad = [(b, v.details) for b, v in enumerate(verdicts) if not v.ok]
+    assert not bad, bad[:4]
