@@ -105,6 +105,11 @@ def test_outputs_match_oracle(name):
         else:
             assert torch.equal(filt[b], rf), b
         rp = F.softmax(rf, dim=-1)
+        # against the exact (float64) softmax of the filtered logits: torch's
+        # float32 CPU softmax itself can be ~5e-5 relative off on long rows
+        rp64 = F.softmax(rf.double(), dim=-1)
+        tol64 = (1e-6 if is32 else 1e-2) * rp64.abs() + (2.0 ** -24 if rf.dtype == torch.float16 else 1e-37)
+        assert bool(((probs[b].double() - rp64).abs() <= tol64).all()), (b, float((probs[b].double() - rp64).abs().max()))
         if is32:
             err = (probs[b].double() - rp.double()).abs()
             # (below FLT_MIN a probability is zero for every purpose)
