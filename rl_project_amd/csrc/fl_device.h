@@ -112,9 +112,18 @@ __device__ __forceinline__ float f32_of_key(uint32_t k) {
 // soft-cap tanh(x / c) * c  (models/attention/causal.py:109-110): three ops.
 template <class D>
 __device__ __forceinline__ float softcap_val(float x, float cap) {
-  const float a = D::rn(x / cap);
-  const float t = D::rn(tanhf(a));
-  return D::rn(t * cap);
+  if constexpr (D::id == FL_DTYPE_F32) {
+    // float32 rows: x / cap as x * (1 / cap) (1 / cap is loop-invariant and
+    // hoisted), at most an ulp from the quotient -- below the ulp by which
+    // tanhf already differs from the reference's tanh; the soft-cap is an
+    // extension of the reference sampler.  Every kernel applies this same
+    // function, so their values agree bit for bit.
+    return tanhf(x * (1.0f / cap)) * cap;
+  } else {
+    const float a = D::rn(x / cap);
+    const float t = D::rn(tanhf(a));
+    return D::rn(t * cap);
+  }
 }
 
 // repetition penalty on one value (sampling.py:30): x>0 ? x/rp : x*rp.
