@@ -14,8 +14,9 @@ pytestmark = pytest.mark.gpu
 def _close(got, ref, atol, rtol=1e-5):
     got, ref = got.cpu().double(), ref.double()
     both_nan = torch.isnan(got) & torch.isnan(ref)
-    ok = both_nan | ((got - ref).abs() <= atol + rtol * ref.abs())
-    return bool(ok.all()), float(((got - ref).abs()[~both_nan]).max()) if bool((~both_nan).any()) else 0.0
+    # (equal infinities: a label on a -inf logit has log-probability -inf)
+    ok = both_nan | (got == ref) | ((got - ref).abs() <= atol + rtol * ref.abs())
+    return bool(ok.all()), float(((got - ref).abs()[~ok]).max()) if bool((~ok).any()) else 0.0
 
 
 @pytest.mark.parametrize("dtype,shape,scale", [
@@ -79,3 +80,31 @@ def test_neg_inf_and_bad_labels():
     assert _close(st.logprob, L.token_logprobs_from_logits(x, lab), 2e-5)[0]
     with pytest.raises(IndexError):
         token_logprobs_from_logits(x.cuda(), torch.tensor([3, 1000, 1, 2]).cuda())
+
+
+def test_random_row_stats_cases():
+    """Seeded random shapes, dtypes and value ranges, with -inf entries and
+    ignored targets: every statistic within the tolerances above."""
+    import random
+    for seed in range(40):
+        rng = random.Random(seed)
+        dt = rng.choice([torch.float32, torch.bfloat16, torch.float16])
+        R = rng.choice([1, 7, 33])
+        V = rng.choice([2, 100, 4099, 50257, 151936])
+        scale = rng.choice([0.1, 1.0, 5.0, 20.0])
+        g = torch.Generator().manual_seed(seed)
+        x = scale * torch.randn(R, V, generator=g)
+        y = x + rng.choice([0.0, 0.1, 2.0]) * torch.randn(R, V, generator=g)
+        if rng.random() < 0.3:
+            x[torch.rand(R, V, generator=g) < 0.2] = float("-inf")
+            x[:, 0] = 0.0
+        x, y = x.to(dt), y.to(dt)
+        lab = torch.randint(0, V, (R,), generator=g)
+        lab[torch.rand(R, generator=g) < 0.2] = -100
+        print(f"[random row stats] seed={seed} {dt} R={R} V={V}", flush=True)
+        st = row_stats(x.cuda(), lab.cuda(), y.cuda(), entropy=True, lse=True)
+        torch.cuda.synchronize()
+        assert _close(st.logprob, L.token_logprobs_from_logits(x, lab), 2e-5)[0], seed
+        assert _close(st.entropy, L.entropy_from_logits(x), 2e-5)[0], seed
+        assert _close(st.kl, L.kl_full_distribution(x, y), 2e-5)[0], seed
+        assert _close(st.lse, L.logsumexp(x), 2e-5, 1e-6)[0], seed
