@@ -636,7 +636,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       int L = N;
       if (K > 0 && K < V) {
         // first entry whose inclusive count reaches K; every equal value stays
-        const int ik = wave_first(0, N, [&](int i) { return count_before(i + 1) >= static_cast<uint32_t>(K); });
+        // (every entry counts at least one value, so the K-th value lies in
+        // the first K entries: one probe round for K <= 64)
+        const int ik = wave_first(0, min(N, K), [&](int i) { return count_before(i + 1) >= static_cast<uint32_t>(K); });
         // (k beyond the finite values: the k-th largest is -inf, every
         // finite value stays)
         if (ik < N) L = group_hi(ik, Y(ik)) + 1;
