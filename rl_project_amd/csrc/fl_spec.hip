@@ -104,45 +104,55 @@ struct SharedSpec {
   int32_t token;
 };
 
-// Accept walk of sequence b (one thread): ratio = min(1, p(d)/(q(d)+1e-10))
+// Accept walk of sequence b (one wave): ratio = min(1, p(d)/(q(d)+1e-10))
 // in the logits' dtype (:63), accept iff u_accept < ratio (:65).  Writes the
 // ratios and the accepted drafts; returns the accepted count, *rej = whether
 // a draft was rejected.
 template <class D>
 __device__ int accept_walk(const fl_spec_args& a, int64_t b, bool* rej) {
+  // Called by one whole wave: lane l evaluates positions l, l + 64, ... in
+  // parallel (their loads in flight together); the first position whose
+  // draw fails the ratio ends the walk, as the sequential rule has it.
   using C = Chunk<D>;
+  const int lane = threadIdx.x & (WAVE - 1);
   const int64_t K = a.k;
   const int V = static_cast<int>(a.vocab);
   const float T = a.temperature[b];
   const size_t esz = D::id == FL_DTYPE_F32 ? 4 : 2;
-  int n = 0;
-  *rej = false;
-  for (int64_t i = 0; i < K; ++i) {
-    const int64_t d = a.draft_ids[b * K + i];
+  int64_t n = K;  // accepted drafts (the first rejected position, if any)
+  for (int64_t i0 = 0; i0 < K && n == K; i0 += WAVE) {
+    const int64_t i = i0 + lane;
     float ratio = 0.0f;
-    if (d >= 0 && d < V) {
-      const fl_row_desc td = a.target_desc[b * (K + 1) + i];
-      const fl_row_desc dd = a.draft_desc[b * K + i];
-      const char* tp = static_cast<const char*>(a.target) + (b * (K + 1) + i) * a.ld * esz;
-      const char* dp = static_cast<const char*>(a.draft) + (b * K + i) * a.ld * esz;
-      const __amdgpu_buffer_rsrc_t rt = row_rsrc(tp, static_cast<uint32_t>(V * esz));
-      const __amdgpu_buffer_rsrc_t rd = row_rsrc(dp, static_cast<uint32_t>(V * esz));
-      const float p = prob_of<D>(td, filt_value<D>(C::elem(rt, static_cast<int>(d)), a.softcap, T), d);
-      const float q = prob_of<D>(dd, filt_value<D>(C::elem(rd, static_cast<int>(d)), a.softcap, T), d);
-      ratio = fminf(1.0f, D::rn(p / D::rn(q + 1e-10f)));
+    int64_t d = -1;
+    bool acc = false;
+    if (i < K) {
+      d = a.draft_ids[b * K + i];
+      if (d >= 0 && d < V) {
+        const fl_row_desc td = a.target_desc[b * (K + 1) + i];
+        const fl_row_desc dd = a.draft_desc[b * K + i];
+        const char* tp = static_cast<const char*>(a.target) + (b * (K + 1) + i) * a.ld * esz;
+        const char* dp = static_cast<const char*>(a.draft) + (b * K + i) * a.ld * esz;
+        const __amdgpu_buffer_rsrc_t rt = row_rsrc(tp, static_cast<uint32_t>(V * esz));
+        const __amdgpu_buffer_rsrc_t rd = row_rsrc(dp, static_cast<uint32_t>(V * esz));
+        const float p = prob_of<D>(td, filt_value<D>(C::elem(rt, static_cast<int>(d)), a.softcap, T), d);
+        const float q = prob_of<D>(dd, filt_value<D>(C::elem(rd, static_cast<int>(d)), a.softcap, T), d);
+        ratio = fminf(1.0f, D::rn(p / D::rn(q + 1e-10f)));
+      }
+      acc = a.u_accept[b * K + i] < ratio;
     }
-    if (a.out_ratio) a.out_ratio[b * K + i] = ratio;
-    if (a.u_accept[b * K + i] < ratio) {
-      a.out_tokens[b * (K + 1) + i] = d;
-      ++n;
-    } else {
-      *rej = true;
-      break;
+    const uint64_t fail = __ballot(i < K && !acc);
+    const int64_t f = fail ? i0 + __ffsll(static_cast<unsigned long long>(fail)) - 1 : K;
+    if (i < K) {
+      if (a.out_ratio) a.out_ratio[b * K + i] = i <= f ? ratio : __builtin_nanf("");
+      if (i < f) a.out_tokens[b * (K + 1) + i] = d;
     }
+    n = f;
   }
-  if (a.out_ratio)
-    for (int64_t i = n + (*rej ? 1 : 0); i < K; ++i) a.out_ratio[b * K + i] = __builtin_nanf("");
-  return n;
+  // (positions of rounds after the rejecting one: no ratio)
+  if (a.out_ratio && n < K)
+    for (int64_t i = (n / WAVE + 1) * WAVE + lane; i < K; i += WAVE) a.out_ratio[b * K + i] = __builtin_nanf("");
+  *rej = n < K;
+  return static_cast<int>(n);
 }
 
 // The target and draft rows of one position and their filtered probabilities.
@@ -361,10 +371,13 @@ __global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
   __shared__ SharedSpec sh;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
-  if (tid == 0) {
+  if (tid < WAVE) {
     bool rej;
-    sh.n_acc = accept_walk<D>(a, b, &rej);
-    sh.rejected = rej ? 1 : 0;
+    const int n = accept_walk<D>(a, b, &rej);
+    if (tid == 0) {
+      sh.n_acc = n;
+      sh.rejected = rej ? 1 : 0;
+    }
   }
   __syncthreads();
   const int n_acc = sh.n_acc;
@@ -389,9 +402,9 @@ __global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
 template <class D>
 __global__ __launch_bounds__(WAVE) void k_spec_accept(const fl_spec_args a, SpecWs ws) {
   const int64_t b = blockIdx.x;
-  if (threadIdx.x != 0) return;
   bool rej;
   const int n = accept_walk<D>(a, b, &rej);
+  if (threadIdx.x != 0) return;
   ws.state[b] = rej ? n : -1;
   if (rej) a.out_n_accepted[b] = n;
   else write_tail(a, b, n, a.bonus_token[b * (a.k + 1) + a.k]);
