@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package (``rl_project_amd``)
 imports this package; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker or the
-timed CPU baseline -- never as the thing measured or shipped.
+``cpu_baseline`` leg of ``bench.py`` use it, and only as the reference the kernels are
+compared with or the timed CPU baseline -- never as the thing measured or shipped.
 
 Modules
 -------

@@ -1,6 +1,6 @@
 """CPU restatement of the reference's full-distribution log-probability
-statistics (test infrastructure only: the checker of the MI355X kernels,
-never part of the product path).
+statistics (test infrastructure only: the reference the MI355X kernels are
+compared with, never part of the product path).
 
 Each function follows one reference function line by line, in float32 on
 the CPU as the reference computes after ``.float()``:

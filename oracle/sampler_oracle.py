@@ -1,7 +1,8 @@
 """Op-for-op CPU restatement of the reference token sampler (test infrastructure).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
-leg may use this module, and only as the checker / the timed CPU baseline.
+leg may use this module, and only as the reference the kernels are compared
+with / the timed CPU baseline.
 
 The reference sampler is plain PyTorch; its arithmetic *is* the sequence of
 ATen calls it makes.  This restatement therefore performs the same ATen calls,
