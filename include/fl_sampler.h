@@ -56,7 +56,7 @@ enum fl_row_status {
   FL_ROW_ALL_MASKED = 16   /* every logit is -inf: nothing can be sampled */
 };
 
-/* Limits of this build. */
+/* Limits of the library. */
 #define FL_MAX_VOCAB_F32 262144     /* fp32 rows                       */
 #define FL_MAX_VOCAB_16  262144     /* bf16 / fp16 rows (repetition penalty: 131072) */
 #define FL_MAX_HISTORY   65536      /* history ids per row             */

@@ -43,7 +43,7 @@ int validate_sample(const fl_sample_args* a, const char* fn) {
   if (a->vocab < 1) return fail(FL_EINVAL, "%s: vocab %lld < 1", fn, static_cast<long long>(a->vocab));
   const int64_t vmax = a->dtype == FL_DTYPE_F32 ? FL_MAX_VOCAB_F32 : FL_MAX_VOCAB_16;
   if (a->vocab > vmax)
-    return fail(FL_ENOTSUP, "%s: vocab %lld exceeds this build's limit %lld for dtype %d", fn,
+    return fail(FL_ENOTSUP, "%s: vocab %lld exceeds the library's limit %lld for dtype %d", fn,
                 static_cast<long long>(a->vocab), static_cast<long long>(vmax), a->dtype);
   if (a->ld < a->vocab) return fail(FL_EINVAL, "%s: ld %lld < vocab %lld", fn, static_cast<long long>(a->ld),
                                     static_cast<long long>(a->vocab));
@@ -105,7 +105,7 @@ int fl_spec_verify(const fl_spec_args* a, void* stream) {
                 static_cast<long long>(a->batch), static_cast<long long>(a->k), static_cast<long long>(a->vocab),
                 static_cast<long long>(a->ld));
   if (a->vocab > FL_MAX_VOCAB_F32 || a->batch > 0x7fffffff)
-    return fail(FL_ENOTSUP, "fl_spec_verify: vocab %lld or batch %lld beyond this build's limits",
+    return fail(FL_ENOTSUP, "fl_spec_verify: vocab %lld or batch %lld beyond the library's limits",
                 static_cast<long long>(a->vocab), static_cast<long long>(a->batch));
   if (a->batch == 0) return ok();
   if (!a->temperature || !a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
@@ -131,7 +131,7 @@ int fl_row_stats(const fl_row_stats_args* a, void* stream) {
                 static_cast<long long>(a->rows), static_cast<long long>(a->vocab), static_cast<long long>(a->ld),
                 static_cast<long long>(a->ref_ld));
   if (a->vocab > FL_MAX_VOCAB_STATS || a->rows > 0x7fffffff)
-    return fail(FL_ENOTSUP, "fl_row_stats: vocab %lld or rows %lld beyond this build's limits",
+    return fail(FL_ENOTSUP, "fl_row_stats: vocab %lld or rows %lld beyond the library's limits",
                 static_cast<long long>(a->vocab), static_cast<long long>(a->rows));
   if (a->out_kl && !a->ref_logits) return fail(FL_EINVAL, "fl_row_stats: out_kl needs ref_logits");
   if (a->out_logprob && !a->labels) return fail(FL_EINVAL, "fl_row_stats: out_logprob needs labels");

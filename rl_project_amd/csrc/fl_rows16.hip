@@ -93,7 +93,7 @@ __device__ __forceinline__ ScanHit scan_first(Shared16& sh, int n, bool total_gi
   uint64_t carry = 0;
   for (int base = 0; base < n; base += NT) {
     const int i = base + static_cast<int>(threadIdx.x);
-    const bool act = base + w * WAVE < n;  // wave-uniform: this wave holds terms this round
+    const bool act = base + w * WAVE < n;  // wave-uniform: this wave holds terms in this pass
     uint64_t v = 0, inc = 0;
     if (act) {
       v = i < n ? term(i) : 0ull;
