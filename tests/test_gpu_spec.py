@@ -148,3 +148,17 @@ def test_mtp_sampled_tokens_in_range_and_length():
     out = MTPSpeculativeGenerator(model).generate(idx, max_new_tokens=15, temperature=0.9, top_k=40, generator=gen)
     assert out.size(1) == idx.size(1) + 15
     assert bool(((out >= 0) & (out < 1000)).all())
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 151936), (torch.float16, 32000)])
+def test_spec_16_bit_rows(dtype, V):
+    """bf16 / fp16 target and draft logits (a Qwen-sized vocabulary past the
+    16-bit register tile included): ratios, residual and bonus in the dtype."""
+    print(f"[spec {dtype}] B=4 K=3 V={V}", flush=True)
+    w = workloads.make_spec(seed=21, batch=4, vocab=V, k=3, draft_sampler=oracle_draft_sampler(0.8, 0.95))
+    w.target, w.draft = w.target.to(dtype), w.draft.to(dtype)
+    w.draft_ids = oracle_draft_sampler(0.8, 0.95)(w.draft.reshape(-1, V), w.extra["u_draft"]).view(4, 3)
+    out = _run(w)
+    summ, verdicts, ref = classify_spec(w, out.n_accepted, out.tokens)
+    print(summ, out.n_accepted.tolist(), [r.n_accepted for r in ref], flush=True)
+    assert summ["MISMATCH"] == 0, verdicts
