@@ -75,11 +75,15 @@ def _isolated_launches(torch, dev, stream, launch, n: int = ISOLATED):
     return sorted(a.elapsed_time(b) for a, b in ev)
 
 
-def cpu_baseline(w, seconds: float):
+def cpu_baseline(w, seconds: float, got_tokens=None):
     """The oracle's per-row restatement (one [1, V] call per row, as the
     reference inference engine makes them) on the first rows of the workload:
     the median rate of three segments of ``seconds / 3`` with all the threads
-    torch uses, and one segment of ``seconds / 3`` on a single thread."""
+    torch uses, and one segment of ``seconds / 3`` on a single thread.
+
+    ``got_tokens`` (the GPU's tokens for the same batch): the oracle tokens of
+    the rows the baseline sampled are checked against them, outside the timed
+    segments, and the counts are returned under ``parity``."""
     import statistics
 
     import torch
@@ -99,12 +103,15 @@ def cpu_baseline(w, seconds: float):
     O.sample_rows(x[:1], params[:1], u[:1], softcap=w.softcap, want_filtered=False)
     state = {"row": 0}
 
+    oracle_tok = {}
+
     def segment(sec: float) -> float:
         rows = 0
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < sec:
             b = state["row"] % w.batch
-            O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap, want_filtered=False)
+            r = O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap, want_filtered=False)
+            oracle_tok.setdefault(b, r[0].token)
             state["row"] += 1
             rows += 1
         return rows / (time.perf_counter() - t0)
@@ -116,8 +123,11 @@ def cpu_baseline(w, seconds: float):
         one = segment(seconds / 3.0)
     finally:
         torch.set_num_threads(threads)
+    parity = None
+    if got_tokens is not None:
+        parity = _row_parity(w, x, params, u, oracle_tok, got_tokens)
     return {"value": statistics.median(rates), "unit": "rows/s", "cores": threads, "kind": "port",
-            "single_thread_value": one,
+            "single_thread_value": one, "parity": parity,
             "sample": f"{state['row']} rows of {w.name} (seed 0, cycling through its {w.batch} rows), one [1,V] "
                       f"oracle call per row (torch {torch.__version__} CPU, ATEN_CPU_CAPABILITY "
                       f"{torch.backends.cpu.get_cpu_capability()}); value: median of 3 segments of "
@@ -125,7 +135,31 @@ def cpu_baseline(w, seconds: float):
                       f"single_thread_value: one segment of {seconds / 3:.1f} s on 1 thread"}
 
 
-def cpu_baseline_spec(w, seconds: float):
+def _row_parity(w, x, params, u, oracle_tok, got_tokens):
+    """EXACT / TIE / NEAR / CONSEQ / MISMATCH counts of the GPU tokens of the
+    rows the CPU baseline sampled, against its oracle tokens (a differing
+    token is classified with the oracle's keep mask and rounding doubt)."""
+    import torch
+
+    from oracle import classify as C
+    from oracle import sampler_oracle as O
+
+    got = got_tokens.cpu().tolist()
+    counts = {k: 0 for k in ("EXACT", "TIE", "NEAR", "CONSEQ", "MISMATCH")}
+    for b, tok in sorted(oracle_tok.items()):
+        if got[b] == tok:
+            counts["EXACT"] += 1
+            continue
+        ref = O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap)[0]
+        keep = ~torch.isneginf(ref.filtered.float())
+        v = C.classify_row(x[b], params[b], u[b], keep, ref.token, None, got[b], softcap=w.softcap)
+        counts[v.kind] += 1
+    counts["rows_checked"] = len(oracle_tok)
+    counts["batch_rows"] = w.batch
+    return counts
+
+
+def cpu_baseline_spec(w, seconds: float, got=None):
     """The oracle's speculative verify (per sequence: filtered target and draft
     softmax at each examined position, accept test, residual or bonus draw) on
     the first sequences of the workload until ``seconds`` have been spent."""
@@ -137,15 +171,30 @@ def cpu_baseline_spec(w, seconds: float):
     O.speculative_verify(w.target[:1], w.draft[:1], w.draft_ids[:1], p, w.u_accept[:1], w.u_resample[:1])
     seqs = 0
     toks = 0
+    results = {}
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         b = seqs % w.target.size(0)
         r = O.speculative_verify(w.target[b:b + 1], w.draft[b:b + 1], w.draft_ids[b:b + 1], p,
                                  w.u_accept[b:b + 1], w.u_resample[b:b + 1])[0]
+        results.setdefault(b, r)
         toks += r.n_accepted + 1
         seqs += 1
     dt = time.perf_counter() - t0
+    parity = None
+    if got is not None:
+        from oracle import classify as C
+        n_acc, tokens = got[0].cpu().tolist(), got[1].cpu().tolist()
+        counts = {"EXACT": 0, "NEAR": 0, "MISMATCH": 0}
+        for b, r in sorted(results.items()):
+            summ, _, _ = C.classify_spec(w.target[b:b + 1], w.draft[b:b + 1], w.draft_ids[b:b + 1], p,
+                                         w.u_accept[b:b + 1], w.u_resample[b:b + 1], [n_acc[b]], [tokens[b]],
+                                         ref=[r])
+            for k in counts:
+                counts[k] += summ[k]
+        parity = dict(counts, sequences_checked=len(results), batch_sequences=w.target.size(0))
     return {"value": toks / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "parity": parity,
             "sample": f"{seqs} sequences of {w.name} (seed 0, cycling through its {w.target.size(0)}), one oracle "
                       f"verify per sequence (torch {torch.__version__} CPU, {torch.get_num_threads()} threads), "
                       f"{dt:.1f} s"}
@@ -215,7 +264,11 @@ def bench_spec(args, dev) -> int:
                      "kernel": "k_sample_rows32 (target rows) + k_sample_rows32 (draft rows) + k_spec_verify"},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_spec(w, args.cpu_seconds)
+        torch.cuda.synchronize(dev)
+        plans[0].launch()      # the first batch's own outputs, checked against the oracle
+        torch.cuda.synchronize(dev)
+        result["cpu_baseline"] = cpu_baseline_spec(w, args.cpu_seconds, (plans[0].n_accepted, plans[0].tokens))
+        result["parity"] = result["cpu_baseline"]["parity"]
     print(json.dumps(result), flush=True)
     return 0
 
@@ -382,7 +435,10 @@ def main() -> int:
                      "kernel": "k_sample_rows16<BF16, false>" if w.logits.element_size() == 2 else "k_sample_rows32"},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        plans[0].launch()      # the first batch's own tokens, checked against the oracle
+        torch.cuda.synchronize(dev)
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, plans[0].output.tokens.clone())
+        result["parity"] = result["cpu_baseline"]["parity"]
     print(json.dumps(result), flush=True)
     return 0
 

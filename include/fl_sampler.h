@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FL_ABI_VERSION 3
+#define FL_ABI_VERSION 4
 
 enum fl_dtype { FL_DTYPE_F32 = 0, FL_DTYPE_BF16 = 1, FL_DTYPE_F16 = 2 };
 
@@ -97,6 +97,17 @@ typedef struct fl_row_desc {
  * hist_ids may be NULL (no penalty anywhere); if not, hist_len is required and
  * hist_ld == 0 shares one id list between all rows.  finished_in may be NULL.
  * out_logprob, out_status, out_finished and out_desc may be NULL.
+ * uniform_div > 1 lets consecutive rows share a draw: row b reads
+ * uniforms[b / uniform_div] (the K+1 target rows of a speculative sequence
+ * share its resample draw); 0 or 1: one draw per row.
+ * FL_FLAG_APPEND_HISTORY (rows with their own history, hist_ld > 0): after
+ * sampling, row b's token is appended to its history --
+ * hist_ids[b*hist_ld + hist_len[b]] = token, hist_len[b] += 1 -- unless the
+ * row arrived finished (finished_in[b] != 0), failed (token -1) or its
+ * history is full (hist_len[b] >= hist_ld).  hist_ids and hist_len must then
+ * be writable device memory.  The decode-loop bookkeeping of the reference
+ * engine (engine.py:122, the generated id joins the request's tokens) in the
+ * same launch.
  */
 typedef struct fl_sample_args {
   uint32_t struct_size;        /* sizeof(fl_sample_args) */
@@ -125,9 +136,11 @@ typedef struct fl_sample_args {
   int32_t* out_status;
   float* out_logprob;
   fl_row_desc* out_desc;
+  int64_t uniform_div;         /* row b draws with uniforms[b / uniform_div] (<= 1: per row) */
 } fl_sample_args;
 
-#define FL_FLAG_NO_SELECT 1    /* describe the filtered distribution only */
+#define FL_FLAG_NO_SELECT 1       /* describe the filtered distribution only */
+#define FL_FLAG_APPEND_HISTORY 2  /* append each sampled token to its row's history */
 
 /*
  * Batched sample: replaces the per-request loop

@@ -7,16 +7,31 @@ oracle's, except for
                same number of members but different ones (the reference's
                unstable sort leaves the order within a tie group open; the
                oracle and the kernel both keep the lowest indices);
-  * NEAR    -- a decision whose outcome changes when the quantities it
-               compares are perturbed by the oracle's own rounding error
-               (relative ``rel``: PyTorch's CPU softmax is up to ~20 ulp from
-               correctly rounded, float32 cumulative sums of bfloat16
-               probabilities drift, tanh differs by an ulp); the margin is
-               reported;
+  * NEAR    -- a decision that the rounding doubt between the two
+               computations leaves open; the doubt is computed, not assumed:
+                 min-p      the float64 probabilities perturbed by the
+                            kernels' own rounding (``RK`` relative) and the
+                            oracle's own softmax output;
+                 top-p      the gap between the reference's cumulative sums
+                            (sequential float32 for 16-bit rows, float64
+                            rounded to float32 for float32 rows) and exact
+                            sums of correctly rounded probabilities, plus
+                            every earlier probability whose rounding is open;
+                            the group's kept count must lie in the range this
+                            leaves (``_top_p_count_range``);
+                 selection  the draw must fall within the doubt of the
+                            chosen token's cumulative interval
+                            (``selection_near``); greedy picks must be able to
+                            win the first-index argmax under ``RK``
+                            (``greedy_near``);
+               the distance from the boundary is reported;
   * CONSEQ  -- a token difference that follows from an explained mask
                difference (the candidate's token is what the selection rule
                gives on the candidate's mask).
-Anything else is MISMATCH.
+Anything else is MISMATCH.  ``tests/test_classify.py`` plants mistakes
+(an extra token, a top-p cut moved by one value group, a token one position
+off in the inverse CDF, a wrong greedy tie-break, wrong accept / residual /
+bonus draws) and requires MISMATCH for each.
 
 Decision predicates re-evaluated here (reference ``sampling.py:36-61``):
 top-k keeps y >= k-th largest; min-p keeps round(e r) >= round(round(r) min_p)
@@ -36,7 +51,11 @@ import torch.nn.functional as F
 
 from . import sampler_oracle as O
 
-REL = 1e-5
+REL = 1e-5   # kept for callers that pass rel; the decisions use computed doubts
+
+# Relative rounding doubt of one probability as the kernels compute it
+# (exp, one reciprocal and one product in float32: a few ulp), with a margin.
+RK = 1e-6
 
 
 def _rn(x: np.ndarray, dtype: torch.dtype) -> np.ndarray:
@@ -68,6 +87,57 @@ def _perturbed(fn, vals, rel) -> bool:
             if fn(*v) != base:
                 return True
     return False
+
+
+def _top_p_count_range(y: np.ndarray, surv: np.ndarray, grp: np.ndarray, top_p: float, dt) -> tuple:
+    """Range of kept counts of the value group ``grp`` that the top-p rule
+    (``sampling.py:45-51``: sorted position j is removed when
+    ``round(round(C_j) - p_j) >= round(top_p)``) allows under rounding doubt,
+    and the exclusive mass at the group's first member.
+
+    The reference's cumulative sums are the oracle's: sequential float32
+    sums of the dtype-rounded probabilities for 16-bit rows, float64 sums
+    rounded to float32 for float32 rows.  A kernel sums correctly rounded
+    probabilities exactly, up to its own rounding (relative ``RK``).  The
+    doubt at position j is the gap between the two sums there plus every
+    earlier probability whose rounding is open.  Members whose decision holds
+    at both ends of the doubt are certain; kept members form a prefix of the
+    group in sorted order, so the count lies between the certain kept prefix
+    and the members not certainly removed."""
+    vals = torch.from_numpy(np.where(surv, y, -np.inf)).to(dt)
+    srt, order = torch.sort(vals, descending=True, stable=True)
+    ps = F.softmax(srt, dim=-1).double().numpy()
+    p64 = F.softmax(srt.double(), dim=-1).numpy()
+    t = float(_rn(np.float64(top_p), dt))
+    if dt == torch.float32:
+        c_ref = _rn(np.cumsum(ps), dt)
+    else:
+        c_ref = np.cumsum(ps.astype(np.float32), dtype=np.float32).astype(np.float64)
+    pk = _rn(p64, dt)
+    amb = np.abs(_rn(p64 * (1.0 + RK), dt) - _rn(p64 * (1.0 - RK), dt)) + np.abs(ps - pk)
+    c_k = np.cumsum(pk)
+    U = np.abs(c_ref - c_k) + np.cumsum(amb) + 1e-12
+    pos = np.nonzero(np.isin(order.numpy(), grp))[0]
+
+    def removed(c, pp):
+        return bool(_rn(_rn(np.float64(c), dt) - pp, dt) >= t)
+
+    lo_n = hi_n = 0
+    lo_done = hi_done = False
+    for j in pos:
+        outcomes = [removed(c_ref[j] + s1 * U[j], ps[j] + s2 * amb[j]) for s1 in (-1, 0, 1) for s2 in (-1, 0, 1)]
+        if not lo_done:
+            if not any(outcomes):
+                lo_n += 1
+            else:
+                lo_done = True
+        if not hi_done:
+            if not all(outcomes):
+                hi_n += 1
+            else:
+                hi_done = True
+    j0 = pos[0] if pos.size else 0
+    return lo_n, hi_n, float(c_ref[j0] - ps[j0]) if pos.size else 0.0
 
 
 def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tensor, ref_tok: int,
@@ -122,45 +192,20 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 # the same test on the oracle's own softmax output, whose
                 # rounding may differ from the exact value's by one unit
                 keep_or = bool(probs[grp[0]] >= _rn(probs.max() * mp, dt))
-                if _perturbed(lambda a, b: bool(keep_minp(a, b)), [e, r], rel) or keep_or != bool(keep_minp(e, r)):
+                if _perturbed(lambda a, b: bool(keep_minp(a, b)), [e, r], 4 * RK) or keep_or != bool(keep_minp(e, r)):
                     explained = True
                     margins.append(abs(e * r - float(_rn(_rn(r, dt) * mp, dt))) / (e * r))
                     verdict.details.append(f"near min-p y={v:.9g}")
                 del probs
-            # top-p boundary
+            # top-p boundary: the group's kept count must lie in the range
+            # that the rounding doubt of the cumulative sums leaves open
             if not explained and p.top_p is not None and 0 < p.top_p < 1:
-                vals = torch.from_numpy(np.where(surv, y, -np.inf)).to(dt)
-                srt, order = torch.sort(vals, descending=True, stable=True)
-                ps = F.softmax(srt, dim=-1).double().numpy()
-                C = np.cumsum(ps)
-                t = float(_rn(np.float64(p.top_p), dt))
-                pos = np.nonzero(np.isin(order.numpy(), grp))[0]
-                # A probability may come out one unit of the dtype apart on
-                # the two sides: where the oracle's own softmax rounds away from
-                # the correctly rounded value (torch's vectorised float32
-                # softmax on the CPU is up to ~5e-5 relative off), or where the
-                # exact value sits within `rel` of a rounding midpoint.  A
-                # whole group of such members moves the cumulative sums after
-                # it by the group's size in units.
-                p64 = F.softmax(srt.double(), dim=-1).numpy()
-                amb = np.maximum(np.abs(_rn(p64 * (1.0 + rel), dt) - _rn(p64 * (1.0 - rel), dt)),
-                                 np.abs(ps - _rn(p64, dt)))
-                # for 16-bit rows the reference accumulates the cumulative sums
-                # sequentially in float32 (float32 rows: in float64); the
-                # drift from the exact sums adds to the doubt
-                drift = 0.0
-                if dt != torch.float32:
-                    drift = np.abs(np.cumsum(ps.astype(np.float32), dtype=np.float32).astype(np.float64) - C)
-                U = np.cumsum(amb) - amb + drift
-
-                def removed(c, pp):
-                    return bool(_rn(_rn(c, dt) - pp, dt) >= t)
-                for j in pos:
-                    if _perturbed(removed, [C[j], ps[j]], rel) or removed(C[j] - U[j], ps[j]) != removed(C[j] + U[j], ps[j]):
-                        explained = True
-                        margins.append(abs(C[j] - ps[j] - p.top_p) / max(p.top_p, 1e-30))
-                        verdict.details.append(f"near top-p y={v:.9g} excl={C[j] - ps[j]:.9g} top_p={p.top_p}")
-                        break
+                lo_n, hi_n, excl = _top_p_count_range(y, surv, grp, p.top_p, dt)
+                if lo_n <= ng <= hi_n:
+                    explained = True
+                    margins.append(abs(excl - p.top_p) / max(p.top_p, 1e-30))
+                    verdict.details.append(f"near top-p y={v:.9g} excl={excl:.9g} top_p={p.top_p} "
+                                           f"kept {ng} in [{lo_n}, {hi_n}]")
             if not explained:
                 verdict.kind = "MISMATCH"
                 verdict.details.append(f"mask group y={v:.9g} n={grp.size}: ref kept {nr}, got kept {ng}")
@@ -175,32 +220,81 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
             verdict.kind = "CONSEQ" if verdict.kind == "TIE" else verdict.kind
             verdict.details.append(f"token {got_tok} follows from the mask difference")
         else:
-            probs = F.softmax(filt, dim=-1)
             if p.temperature <= 0:
-                pr = probs.double().numpy()
-                m = abs(pr[got_tok] - pr[expect]) / max(pr[expect], 1e-300)
-                ok = pr[got_tok] > 0 and m <= rel * 4
+                ok, m = greedy_near(filt, got_tok, expect)
             else:
-                order = O.selection_order(filt).numpy()
-                pr = probs.double().numpy()[order]
-                C = np.cumsum(pr)
-                target = np.float64(np.float32(u)) * C[-1]
-                jg = int(np.nonzero(order == got_tok)[0][0])
-                lo_c = C[jg - 1] if jg > 0 else 0.0
-                hi_c = C[jg]
-                m = 0.0 if lo_c <= target < hi_c else min(abs(target - lo_c), abs(target - hi_c)) / C[-1]
-                ok = m <= rel
+                ok, m = selection_near(filt, u, got_tok)
             if ok:
                 verdict.kind = "NEAR"
                 margins.append(m)
                 verdict.details.append(f"near selection: token {got_tok} vs {ref_tok}, margin {m:.3g}")
             else:
                 verdict.kind = "MISMATCH"
-                verdict.details.append(f"token {got_tok} vs oracle {ref_tok} (expected {expect} on got mask)")
+                verdict.details.append(f"token {got_tok} vs oracle {ref_tok} (expected {expect} on got mask), "
+                                       f"distance {m:.3g}")
     elif got_tok is not None and got_tok != ref_tok:
         verdict.details.append(f"token {got_tok} vs oracle {ref_tok}")
     verdict.margin = max(margins) if margins else 0.0
     return verdict
+
+
+
+
+def _cdf_doubt(w_oracle: np.ndarray, w_exact: np.ndarray, dt) -> tuple:
+    """Normalised inclusive cumulative sums of the oracle's weights and, per
+    position, how far a kernel's cumulative may lie from them.
+
+    ``w_oracle``: the weights the oracle accumulates (its dtype-rounded
+    probabilities); ``w_exact``: the float64 weights.  A kernel computes each
+    weight correctly rounded to the dtype up to its own rounding (relative
+    ``RK``) and accumulates exactly, so its normalised cumulative differs from
+    the oracle's by the measured gap between the oracle's cumulative and the
+    correctly rounded one, plus the weights whose rounding is open under
+    ``RK``.  Both are summed position by position: the doubt grows only where
+    the two computations can actually differ."""
+    wk = _rn(w_exact, dt)
+    amb = np.abs(_rn(w_exact * (1.0 + RK), dt) - _rn(w_exact * (1.0 - RK), dt))
+    so, sk = float(w_oracle.sum()), float(wk.sum())
+    c_or = np.cumsum(w_oracle) / so
+    c_k = np.cumsum(wk) / sk
+    doubt = np.abs(c_or - c_k) + np.cumsum(amb) / sk + 1e-12
+    return c_or, doubt
+
+
+def selection_near(filt: torch.Tensor, u: float, got_tok: int) -> tuple:
+    """(acceptable, distance) for an inverse-CDF draw that picked ``got_tok``
+    on the filtered row ``filt``: acceptable when the draw ``u`` lies within
+    the rounding doubt of ``got_tok``'s cumulative interval.  The distance is
+    how far ``u`` lies outside the interval (0 inside)."""
+    dt = filt.dtype
+    order = O.selection_order(filt).numpy()
+    ps = F.softmax(filt, dim=-1).double().numpy()[order]
+    p64 = F.softmax(filt.double(), dim=-1).numpy()[order]
+    pos = np.nonzero(order == got_tok)[0]
+    if pos.size == 0 or p64[pos[0]] <= 0.0:
+        return False, float("inf")
+    j = int(pos[0])
+    c, d = _cdf_doubt(ps, p64, dt)
+    t = float(np.float64(np.float32(u)))
+    lo, hi = (c[j - 1], d[j - 1]) if j > 0 else (0.0, 0.0), (c[j], d[j])
+    dist = max(0.0, lo[0] - t, t - hi[0])
+    return bool(lo[0] - lo[1] <= t < hi[0] + hi[1]), dist
+
+
+def greedy_near(filt: torch.Tensor, got_tok: int, expect: int) -> tuple:
+    """(acceptable, relative gap) for a greedy pick: ``got_tok`` may replace
+    the oracle's first maximal probability only if a relative perturbation of
+    ``RK`` of the two float64 probabilities lets it win the first-index
+    argmax of the dtype-rounded values."""
+    dt = filt.dtype
+    p64 = F.softmax(filt.double(), dim=-1).numpy()
+    pg, pe = p64[got_tok], p64[expect]
+    if pg <= 0.0:
+        return False, float("inf")
+    rg = float(_rn(np.array([pg * (1.0 + RK)]), dt)[0])
+    re_ = float(_rn(np.array([pe * (1.0 - RK)]), dt)[0])
+    wins = rg > re_ or (rg == re_ and got_tok < expect)
+    return bool(wins), abs(pe - pg) / pe
 
 
 def summarise(verdicts: List[RowVerdict]) -> dict:
@@ -209,3 +303,108 @@ def summarise(verdicts: List[RowVerdict]) -> dict:
         out[v.kind] += 1
     out["max_margin"] = max([v.margin for v in verdicts] + [0.0])
     return out
+
+
+# --------------------------------------------------------------------------
+# Speculative verify (speculative.py:54-84)
+# --------------------------------------------------------------------------
+
+def _ratio(pv: float, qv: float, dt) -> float:
+    q1 = float(_rn(np.array([float(_rn(np.array([qv]), dt)[0]) + 1e-10]), dt)[0])
+    return min(1.0, float(_rn(np.array([pv / q1]), dt)[0]))
+
+
+def _accept_window(p64: float, q64: float, ratio_oracle: float, u: float, dt) -> tuple:
+    rs = [_ratio(float(_rn(np.array([p64 * a]), dt)[0]), float(_rn(np.array([q64 * c]), dt)[0]), dt)
+          for a in (1.0 - RK, 1.0, 1.0 + RK) for c in (1.0 - RK, 1.0, 1.0 + RK)]
+    lo = min(rs + [ratio_oracle]) * (1.0 - RK)
+    hi = max(rs + [ratio_oracle]) * (1.0 + RK)
+    dist = 0.0 if lo <= u <= hi else min(abs(u - lo), abs(u - hi))
+    return bool(lo <= u <= hi), dist
+
+
+def _residual_doubt(pt: torch.Tensor, pd: torch.Tensor, p64: np.ndarray, q64: np.ndarray) -> tuple:
+    """The oracle's residual weights (``speculative.py:73-74`` as the oracle
+    evaluates them) normalised and cumulated in ascending index order, and the
+    per-position doubt of a kernel that evaluates the same expression on
+    correctly rounded probabilities (up to ``RK``)."""
+    dt = pt.dtype
+    r = torch.clamp(pt - pd, min=0)
+    r = r / (r.sum() + 1e-10)
+    w_or = r.double().numpy()
+    use_p = float(w_or.sum()) <= 0.0
+    if use_p:
+        w_or = pt.double().numpy()
+    pk, qk = _rn(p64, dt), _rn(q64, dt)
+    ambp = np.abs(_rn(p64 * (1.0 + RK), dt) - _rn(p64 * (1.0 - RK), dt))
+    ambq = np.abs(_rn(q64 * (1.0 + RK), dt) - _rn(q64 * (1.0 - RK), dt))
+    if use_p:
+        wk, amb = pk, ambp
+    else:
+        wk = np.maximum(_rn(pk - qk, dt), 0.0)
+        amb = np.where((pk + ambp > qk - ambq), ambp + ambq, 0.0)
+    so, sk = float(w_or.sum()), float(wk.sum())
+    if sk <= 0.0:
+        sk = so
+    c_or = np.cumsum(w_or) / so
+    c_k = np.cumsum(wk) / sk
+    return c_or, np.abs(c_or - c_k) + np.cumsum(amb) / sk + 1e-12
+
+
+def _interval_ok(c: np.ndarray, d: np.ndarray, j: int, t: float) -> tuple:
+    lo, dlo = (c[j - 1], d[j - 1]) if j > 0 else (0.0, 0.0)
+    hi, dhi = c[j], d[j]
+    if hi <= lo:   # an empty interval: a zero weight is never drawn
+        return False, float("inf")
+    return bool(lo - dlo <= t < hi + dhi), max(0.0, lo - t, t - hi)
+
+
+def classify_spec(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, p: O.RowParams,
+                  u_accept: torch.Tensor, u_resample: torch.Tensor, got_n, got_tokens, softcap: float = 0.0,
+                  ref: Optional[List[O.SpecResult]] = None):
+    """Per sequence: EXACT, NEAR (the first difference is an accept decision
+    whose ``u`` lies within the doubt of the ratio, or a resampled / bonus
+    token whose cumulative interval lies within the doubt of the draw) or
+    MISMATCH.  Returns (summary, [(kind, distance)], oracle results)."""
+    if ref is None:
+        ref = O.speculative_verify(target, draft, draft_ids, p, u_accept, u_resample, softcap=softcap)
+    B, K = draft_ids.shape
+    gn = [int(v) for v in got_n]
+    gt = [[int(t) for t in row] for row in got_tokens]
+    out = []
+    for b in range(B):
+        r = ref[b]
+        n = gn[b]
+        toks = gt[b][:n + 1]
+        if n == r.n_accepted and toks == r.tokens:
+            out.append(("EXACT", 0.0))
+            continue
+        m = min(n, r.n_accepted)
+        if n != r.n_accepted or toks[:m] != r.tokens[:m]:
+            if toks[:m] != r.tokens[:m]:
+                out.append(("MISMATCH", float("inf")))
+                continue
+            pt, ft = O.filtered_probs(target[b, m], p, softcap)
+            pd, fd = O.filtered_probs(draft[b, m], p, softcap)
+            d = int(draft_ids[b, m])
+            p64 = float(torch.softmax(ft.double(), -1)[d])
+            q64 = float(torch.softmax(fd.double(), -1)[d])
+            ok, dist = _accept_window(p64, q64, r.accept_ratio[m], float(u_accept[b, m]), pt.dtype)
+            out.append(("NEAR" if ok else "MISMATCH", dist))
+            continue
+        t = float(np.float64(np.float32(u_resample[b])))
+        g = toks[-1]
+        if n < K:   # residual at position n
+            pt, ft = O.filtered_probs(target[b, n], p, softcap)
+            pd, fd = O.filtered_probs(draft[b, n], p, softcap)
+            p64 = torch.softmax(ft.double(), -1).numpy()
+            q64 = torch.softmax(fd.double(), -1).numpy()
+            c, dd = _residual_doubt(pt, pd, p64, q64)
+            ok, dist = _interval_ok(c, dd, g, t) if 0 <= g < c.size else (False, float("inf"))
+        else:       # bonus from target position K
+            _, ft = O.filtered_probs(target[b, K], p, softcap)
+            ok, dist = selection_near(ft, float(u_resample[b]), g)
+        out.append(("NEAR" if ok else "MISMATCH", dist))
+    kinds = [k for k, _ in out]
+    summ = {k: kinds.count(k) for k in ("EXACT", "NEAR", "MISMATCH")}
+    return summ, out, ref

@@ -16,11 +16,12 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflsampler.so")
 
-FL_ABI_VERSION = 3
+FL_ABI_VERSION = 4
 FL_DTYPE_F32, FL_DTYPE_BF16, FL_DTYPE_F16 = 0, 1, 2
 FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
 FL_FLAG_NO_SELECT = 1
+FL_FLAG_APPEND_HISTORY = 2
 FL_MAX_VOCAB_F32 = 262144
 FL_MAX_VOCAB_16 = 262144
 FL_MAX_HISTORY = 65536
@@ -46,6 +47,7 @@ class SampleArgs(ctypes.Structure):
         ("stop_ids", _p), ("stop_ld", ctypes.c_int64), ("n_stop", ctypes.c_int64),
         ("uniforms", _p), ("finished_in", _p),
         ("out_token", _p), ("out_finished", _p), ("out_status", _p), ("out_logprob", _p), ("out_desc", _p),
+        ("uniform_div", ctypes.c_int64),
     ]
 
 

@@ -53,6 +53,12 @@ int validate_sample(const fl_sample_args* a, const char* fn) {
     return fail(FL_EINVAL, "%s: hist_ids needs hist_len and hist_ld >= 0", fn);
   if (a->n_stop < 0 || (a->n_stop > 0 && (a->stop_ids == nullptr || a->stop_ld < 0)))
     return fail(FL_EINVAL, "%s: stop_ids/n_stop/stop_ld inconsistent", fn);
+  if ((a->flags & ~(FL_FLAG_NO_SELECT | FL_FLAG_APPEND_HISTORY)) != 0)
+    return fail(FL_EINVAL, "%s: unknown flags 0x%x", fn, static_cast<unsigned>(a->flags));
+  if (a->uniform_div < 0) return fail(FL_EINVAL, "%s: uniform_div %lld < 0", fn, static_cast<long long>(a->uniform_div));
+  if ((a->flags & FL_FLAG_APPEND_HISTORY) &&
+      (a->hist_ids == nullptr || a->hist_ld <= 0 || (a->flags & FL_FLAG_NO_SELECT)))
+    return fail(FL_EINVAL, "%s: FL_FLAG_APPEND_HISTORY needs per-row histories (hist_ld > 0) and a selection", fn);
   if (a->batch > 0 && (a->temperature == nullptr || a->top_k == nullptr || a->top_p == nullptr ||
                        a->min_p == nullptr || a->rep_penalty == nullptr))
     return fail(FL_EINVAL, "%s: the per-row parameter arrays (temperature, top_k, top_p, min_p, rep_penalty) "

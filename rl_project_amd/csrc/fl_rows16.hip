@@ -211,7 +211,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const float TP = a.top_p[b];
   const float MP = a.min_p[b];
   const float RP = a.rep_penalty[b];
-  const float U_in = (select ? a.uniforms : a.temperature)[b];
+  const int64_t ub = a.uniform_div > 1 ? b / a.uniform_div : b;  // rows sharing a draw
+  const float U_in = (select ? a.uniforms : a.temperature)[select ? ub : b];
   const int H_in = (a.hist_ids ? a.hist_len : dummy)[b];
   __builtin_amdgcn_sched_barrier(0);
   const bool hist_rows = a.hist_ids != nullptr && a.hist_ld > 0;   // one id list per row
@@ -1114,8 +1115,18 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     if (a.out_logprob) {
       float lp = __builtin_nanf("");
-      if (tok >= 0) lp = D::rn((y_sel - M) - logf(static_cast<float>(SK)));
+      // log_softmax(filtered)[tok] as torch evaluates it on a 16-bit tensor
+      // (sampling.py:97-98): the kept mass and its log each rounded to the
+      // dtype, then y - max - log, rounded
+      if (tok >= 0) lp = D::rn((y_sel - M) - D::rn(logf(D::rn(static_cast<float>(SK)))));
       a.out_logprob[b] = lp;
+    }
+    if ((a.flags & FL_FLAG_APPEND_HISTORY) && hist_rows && tok >= 0 &&
+        !(a.finished_in != nullptr && a.finished_in[b] != 0) && H_in >= 0 && H_in < a.hist_ld) {
+      // (every read of this row's history, all below index H_in, finished
+      // before the barriers that led here)
+      const_cast<int32_t*>(a.hist_ids)[b * a.hist_ld + H_in] = static_cast<int32_t>(tok);
+      const_cast<int32_t*>(a.hist_len)[b] = H_in + 1;
     }
     if (a.out_desc) {
       fl_row_desc dsc;

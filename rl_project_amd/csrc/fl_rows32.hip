@@ -994,7 +994,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const float TP = a.top_p[b];
   const float MP = a.min_p[b];
   const float RP = a.rep_penalty[b];
-  const float U_in = select ? a.uniforms[b] : 0.0f;
+  const float U_in = select ? a.uniforms[a.uniform_div > 1 ? b / a.uniform_div : b] : 0.0f;
   const int H_in = a.hist_ids ? a.hist_len[b] : 0;
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const bool hist_too_long = H_in > FL_MAX_HISTORY;
@@ -1444,6 +1444,27 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const uint32_t keep_n = o.keep_n;
   const double SK = from_fx45(o.keep_mass);
   const float rK = 1.0f / static_cast<float>(SK);
+  // Greedy (sampling.py:59-60) is torch.argmax of the float32 probabilities:
+  // the first index among equal probabilities.  Values a few ulp below the
+  // maximum M (|M| small, so that exp(y - M) rounds to 1) can share the
+  // maximum's probability; the token is then the lowest such kept index.
+  // Rows whose next value below M already has a smaller probability (every
+  // row with |M| >= 0.25) skip the pass.
+  if (select && T <= 0.0f && status == 0 && tok >= 0) {
+    const float below = f32_of_key(f32_key(M) - 1u);  // the next float below M (M is finite)
+    if (expf(below - M) * rK == rK) {
+      const float ycut = f32_of_key(static_cast<uint32_t>(CK >> 32));
+      const uint32_t lowc = static_cast<uint32_t>(CK);
+      const int icut = lowc == 0u ? INT_MAX : static_cast<int>(~lowc);
+      int best = static_cast<int>(tok);
+      row_pass(S, X, [&](int idx, float y, bool valid) {
+        const bool kept = y > ycut || (y == ycut && idx <= icut);
+        if (valid && kept && idx < best && y < M && expf(y - M) * rK == rK) best = idx;
+      });
+      best = block_reduce<int32_t>(best, OpMin(), sh.redi);
+      tok = best;
+    }
+  }
   float y_sel = 0.0f;
   if (tid == 0 && status == 0 && tok >= 0) {
     const int i = static_cast<int>(tok);
@@ -1464,6 +1485,13 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
       float lp = __builtin_nanf("");
       if (tok >= 0) lp = (y_sel - M) - logf(static_cast<float>(SK));
       a.out_logprob[b] = lp;
+    }
+    if ((a.flags & FL_FLAG_APPEND_HISTORY) && a.hist_ids != nullptr && a.hist_ld > 0 && tok >= 0 &&
+        !(a.finished_in != nullptr && a.finished_in[b] != 0) && H_in >= 0 && H_in < a.hist_ld) {
+      // (every read of this row's history, all below index H_in, finished
+      // before the barriers that led here)
+      const_cast<int32_t*>(a.hist_ids)[b * a.hist_ld + H_in] = static_cast<int32_t>(tok);
+      const_cast<int32_t*>(a.hist_len)[b] = H_in + 1;
     }
     if (a.out_desc) {
       fl_row_desc dsc;

@@ -15,28 +15,35 @@ EOS id as its stop set (``engine.py:123-125``).
 * the history ids, with capacity ``max_seq_len``;
 * the stop set.
 
-``step(logits)`` samples every active slot in one launch and appends the
-tokens to the histories on the device. It returns device tensors; the caller
+``step(logits)`` samples every row in one launch; the kernel also sets the
+finished flags and appends the tokens to the histories (no host
+synchronisation, no other kernel). It returns device tensors; the caller
 reads them back once per step, not once per sequence. Length limits,
 cancellation and block allocation stay with the engine, as in the reference.
 """
 
 from __future__ import annotations
 
-from typing import Iterable, List, Optional, Sequence
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 import torch
 
 from .params import SamplingParams
-from .sampling import SampleOutput, sample_tokens
+from . import _lib
+from .sampling import SampleOutput, _Call, _check_logits
 
 
 class BatchedSampler:
     """Device-resident sampling state of up to ``max_rows`` sequences.
 
-    Slots ``0 .. n-1`` of a step are the first ``n`` rows of the logits, in
-    the order the engine stacks its decode group; ``admit`` / ``release``
-    manage which request holds which slot."""
+    Row ``i`` of a step's logits belongs to slot ``i`` (or to ``slots[i]`` when
+    the step names its slots); ``admit`` / ``release`` manage which request
+    holds which slot.  A step is one ``fl_sample`` launch: the kernel samples
+    every row, sets the finished flags in place and appends each token to its
+    slot's history (``FL_FLAG_APPEND_HISTORY``); nothing is synchronised with
+    the host and nothing is allocated (the argument block and the output
+    buffers are kept per row count and reused, so a step's outputs are valid
+    until the next step)."""
 
     def __init__(self, max_rows: int, max_seq_len: int, vocab: int, device, *, eos_token_id: Optional[int] = None,
                  max_stop_ids: int = 8, generator: Optional[torch.Generator] = None):
@@ -53,9 +60,14 @@ class BatchedSampler:
         self.history = torch.full((max_rows, max_seq_len), -1, dtype=torch.int32, device=d)
         self.hist_len = torch.zeros(max_rows, dtype=torch.int32, device=d)
         self.stop_ids = torch.full((max_rows, max_stop_ids + 1), -1, dtype=torch.int32, device=d)
-        self.finished = torch.zeros(max_rows, dtype=torch.bool, device=d)
-        self._host_len: List[int] = [0] * max_rows
-        self._rows = torch.arange(max_rows, device=d)
+        # uint8, updated in place by the kernel (finished_in and out_finished)
+        self.finished_u8 = torch.ones(max_rows, dtype=torch.uint8, device=d)
+        self._plans: Dict[Tuple[int, torch.dtype, int, int, bool], _Call] = {}
+
+    @property
+    def finished(self) -> torch.Tensor:
+        """bool [max_rows]: slots that produced a stop id or were released."""
+        return self.finished_u8.view(torch.bool)
 
     def admit(self, slot: int, params: SamplingParams, prompt_tokens: Sequence[int]) -> None:
         """Give ``slot`` to a new request: its parameters (validated as
@@ -83,35 +95,70 @@ class BatchedSampler:
         if stops:
             srow[:len(stops)] = torch.tensor(stops, dtype=torch.int32)
         self.stop_ids[slot].copy_(srow)
-        self.finished[slot] = False
-        self._host_len[slot] = n
+        self.finished_u8[slot] = 0
 
     def release(self, slot: int) -> None:
-        self.finished[slot] = True
+        """Retire ``slot``: it is finished (a row of a later step that still
+        maps to it samples but appends nothing) and its history is emptied."""
+        self.finished_u8[slot] = 1
+        self.hist_len[slot] = 0
 
-    def step(self, logits: torch.Tensor, uniforms: Optional[torch.Tensor] = None,
-             return_logprobs: bool = False) -> SampleOutput:
-        """Sample one token for each of the first ``logits.size(0)`` slots and
-        append it to their histories (device only, no host synchronisation)."""
+    def _plan(self, n: int, logits: torch.Tensor, want_logprob: bool) -> _Call:
+        key = (n, logits.dtype, logits.size(1), logits.stride(0), want_logprob)
+        call = self._plans.get(key)
+        if call is None:
+            call = _Call(logits, temperature=self.temperature[:n], top_k=self.top_k[:n], top_p=self.top_p[:n],
+                         min_p=self.min_p[:n], repetition_penalty=self.rep_penalty[:n],
+                         history=(self.history[:n], self.hist_len[:n]), stop_ids=self.stop_ids[:n],
+                         uniforms=torch.zeros(n, dtype=torch.float32, device=self.device),
+                         finished=self.finished_u8[:n], out_finished=self.finished_u8[:n],
+                         flags=_lib.FL_FLAG_APPEND_HISTORY, want_logprob=want_logprob)
+            # the state tensors are used in place, never copied
+            assert call.hist.data_ptr() == self.history.data_ptr() and call.fin_in.data_ptr() == \
+                self.finished_u8.data_ptr()
+            self._plans[key] = call
+        return call
+
+    def step(self, logits: torch.Tensor, uniforms: Optional[torch.Tensor] = None, return_logprobs: bool = False,
+             slots: Optional[torch.Tensor] = None) -> SampleOutput:
+        """Sample one token for each row of ``logits`` (row i: slot i, or
+        ``slots[i]``), mark the rows that produced a stop id as finished and
+        append the tokens of unfinished rows to their histories, in one launch
+        with no host synchronisation.  ``status`` of the output carries the
+        per-row FL_ROW_* bits for the caller to read with the tokens."""
         n = logits.size(0)
         if n > self.max_rows:
             raise ValueError(f"{n} rows exceed max_rows {self.max_rows}")
-        if max(self._host_len[:n], default=0) >= self.max_seq_len:
-            raise ValueError("a history is full: retire the sequence before max_seq_len")
         if uniforms is None:
             uniforms = torch.rand(n, device=self.device, generator=self.generator)
-        out = sample_tokens(logits, temperature=self.temperature[:n], top_k=self.top_k[:n], top_p=self.top_p[:n],
-                            min_p=self.min_p[:n], repetition_penalty=self.rep_penalty[:n],
-                            history=(self.history[:n], self.hist_len[:n]), stop_ids=self.stop_ids[:n],
-                            uniforms=uniforms, finished=self.finished[:n], return_logprobs=return_logprobs)
-        # append to the histories on the device
-        rows = self._rows[:n]
-        self.history[rows, self.hist_len[:n].long()] = out.tokens.to(torch.int32)
-        self.hist_len[:n] += 1
-        self.finished[:n] = out.finished
-        for i in range(n):
-            self._host_len[i] += 1
-        return out
+        if slots is not None:
+            return self._step_slots(logits, uniforms, return_logprobs, slots)
+        logits = _check_logits(logits)
+        call = self._plan(n, logits, return_logprobs)
+        if uniforms.dtype != torch.float32 or not uniforms.is_contiguous() or uniforms.numel() != n:
+            raise ValueError("uniforms must be a contiguous float32 tensor with one draw per row")
+        call.args.logits = logits.data_ptr()
+        call.args.uniforms = uniforms.data_ptr()
+        call.keep = (logits, uniforms)   # alive until the kernel has read them
+        call.run()
+        return SampleOutput(call.tokens, call.finished[:n].view(torch.bool), call.status, call.logprob)
+
+    def _step_slots(self, logits, uniforms, return_logprobs, slots) -> SampleOutput:
+        """A decode group whose rows map to arbitrary slots: gather the slots'
+        state, sample with the append, scatter the state back (a few small
+        device copies; no host synchronisation)."""
+        idx = slots.to(device=self.device, dtype=torch.long)
+        hist = self.history.index_select(0, idx)
+        hlen = self.hist_len.index_select(0, idx)
+        fin = self.finished_u8.index_select(0, idx)
+        call = _Call(logits, temperature=self.temperature[idx], top_k=self.top_k[idx], top_p=self.top_p[idx],
+                     min_p=self.min_p[idx], repetition_penalty=self.rep_penalty[idx], history=(hist, hlen),
+                     stop_ids=self.stop_ids[idx], uniforms=uniforms, finished=fin, out_finished=fin,
+                     flags=_lib.FL_FLAG_APPEND_HISTORY, want_logprob=return_logprobs).run()
+        self.history.index_copy_(0, idx, hist)
+        self.hist_len.index_copy_(0, idx, hlen)
+        self.finished_u8.index_copy_(0, idx, fin)
+        return SampleOutput(call.tokens, fin.view(torch.bool), call.status, call.logprob)
 
     def history_of(self, slot: int) -> List[int]:
         """Prompt + generated ids of a slot (reads the device: for tests and retirement)."""

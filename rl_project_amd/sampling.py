@@ -137,7 +137,8 @@ class _Call:
     def __init__(self, logits: torch.Tensor, *, temperature: PerRow = 1.0, top_k: PerRow = None,
                  top_p: PerRow = None, min_p: PerRow = None, repetition_penalty: PerRow = 1.0, history=None,
                  stop_ids=None, uniforms: Optional[torch.Tensor] = None, finished: Optional[torch.Tensor] = None,
-                 softcap: float = 0.0, flags: int = 0, want_logprob: bool = False, want_desc: bool = False):
+                 softcap: float = 0.0, flags: int = 0, want_logprob: bool = False, want_desc: bool = False,
+                 uniform_div: int = 1, out_finished: Optional[torch.Tensor] = None):
         self.logits = logits = _check_logits(logits)
         B, V = logits.shape
         dev = logits.device
@@ -150,14 +151,21 @@ class _Call:
         self.hist, self.hist_len, self.hist_ld = _history_tensor(history, B, V, dev)
         self.stop, self.stop_ld, self.n_stop = _stop_tensor(stop_ids, B, dev)
         select = not (flags & FL_FLAG_NO_SELECT)
+        uniform_div = max(1, int(uniform_div))
+        n_draws = (B + uniform_div - 1) // uniform_div
         if uniforms is None and select:
-            uniforms = torch.rand(B, device=dev, dtype=torch.float32)
+            uniforms = torch.rand(n_draws, device=dev, dtype=torch.float32)
         self.U = None if uniforms is None else uniforms.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
-        if self.U is not None and self.U.numel() != B:
-            raise ValueError(f"uniforms has {self.U.numel()} entries for {B} rows")
+        if self.U is not None and self.U.numel() != n_draws:
+            raise ValueError(f"uniforms has {self.U.numel()} entries for {B} rows ({n_draws} draws)")
+        if flags & _lib.FL_FLAG_APPEND_HISTORY and (self.hist is None or self.hist_ld <= 0 or B > 1 and
+                                                    self.hist.stride(0) != self.hist_ld):
+            raise ValueError("appending to the histories needs a per-row (ids, lengths) history")
         self.fin_in = None if finished is None else finished.to(device=dev, dtype=torch.uint8).reshape(-1).contiguous()
         self.tokens = torch.empty(B, dtype=torch.int64, device=dev)
-        self.finished = torch.empty(B, dtype=torch.uint8, device=dev)
+        # (out_finished may be the finished_in buffer itself: each row reads its
+        # flag before writing it)
+        self.finished = out_finished if out_finished is not None else torch.empty(B, dtype=torch.uint8, device=dev)
         self.status = torch.empty(B, dtype=torch.int32, device=dev)
         self.logprob = torch.empty(B, dtype=torch.float32, device=dev) if want_logprob else None
         self.desc = torch.empty(B, ROW_DESC_BYTES, dtype=torch.uint8, device=dev) if want_desc else None
@@ -175,6 +183,7 @@ class _Call:
         a.uniforms, a.finished_in = ptr(self.U), ptr(self.fin_in)
         a.out_token, a.out_finished, a.out_status = ptr(self.tokens), ptr(self.finished), ptr(self.status)
         a.out_logprob, a.out_desc = ptr(self.logprob), ptr(self.desc)
+        a.uniform_div = uniform_div
         self.args = a
         self.stream = _lib.stream_handle(dev)
 

@@ -74,7 +74,9 @@ class SpecPlan:
                     softcap=softcap)
         tgt = _check_logits(target_logits.reshape(B * K1, V))
         drf = _check_logits(draft_logits.reshape(B * K, V))
-        self._t = _Call(tgt, flags=0, want_desc=True, uniforms=self.u_resample.repeat_interleave(K1), **filt)
+        # the K+1 target rows of a sequence share its resample draw (read at
+        # launch time, so in-place updates of u_resample reach the bonus draw)
+        self._t = _Call(tgt, flags=0, want_desc=True, uniforms=self.u_resample, uniform_div=K1, **filt)
         self._d = _Call(drf, flags=FL_FLAG_NO_SELECT, want_desc=True, uniforms=None, **filt)
         self.n_accepted = torch.empty(B, dtype=torch.int32, device=dev)
         self.tokens = torch.empty(B, K1, dtype=torch.int64, device=dev)

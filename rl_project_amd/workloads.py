@@ -91,6 +91,7 @@ class SpecWorkload:
     temperature: float = 0.8
     top_p: float = 0.95
     extra: Dict[str, object] = field(default_factory=dict)
+    top_k: int = 0                # 0 = off (the reference's default speculative filter is top-k 50)
 
     def algorithmic_bytes(self) -> int:
         B, K = self.draft_ids.shape
@@ -100,7 +101,7 @@ class SpecWorkload:
     def to(self, device) -> "SpecWorkload":
         return SpecWorkload(self.name, self.target.to(device), self.draft.to(device), self.draft_ids.to(device),
                             self.u_accept.to(device), self.u_resample.to(device), self.temperature, self.top_p,
-                            dict(self.extra))
+                            dict(self.extra), self.top_k)
 
 
 def zipf_ids(g: torch.Generator, shape, V: int, s: float) -> torch.Tensor:

@@ -1,0 +1,278 @@
+"""The parity classifier has teeth: planted mistakes must come out MISMATCH,
+and only rounding-level differences may come out NEAR (CPU only).
+
+Every GPU parity test accepts TIE / NEAR / CONSEQ on the word of
+``oracle.classify``; these tests plant the mistakes a kernel could plausibly
+make -- an extra kept token, a top-p cut moved by one value group, a kept
+count of a partial group outside the rounding range, a token one position off
+in the inverse CDF, a wrong greedy tie-break, a wrong accept decision, a
+residual or bonus token one position off -- and require MISMATCH for each,
+at the sizes the benchmark runs (V = 128256 bf16 rows, V = 262144 fp32)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import classify as C
+from oracle import sampler_oracle as O
+
+V = 128256
+
+
+def _bf16_row(seed, scale=2.5):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(V, generator=g) * scale).to(torch.bfloat16)
+    hist = torch.randint(0, V, (2048,), generator=g).tolist()
+    return x, hist
+
+
+def _oracle(x, p, u, softcap=0.0):
+    r = O.sample_rows(x[None], [p], [u], softcap=softcap)[0]
+    keep = ~torch.isneginf(r.filtered.float())
+    hist = p.history if p.repetition_penalty != 1.0 else None
+    y = O.pre_filter_values(x[None], p.temperature, p.repetition_penalty, hist, softcap)[0]
+    return r, keep, y
+
+
+def _kind(x, p, u, keep, tok, got_keep, got_tok, softcap=0.0):
+    return C.classify_row(x, p, u, keep, tok, got_keep, got_tok, softcap=softcap)
+
+
+# wide nuclei: top-p is the binding cut and spans tens of thousands of tokens
+WIDE = [(1.5, 0.9), (1.0, 0.95), (1.2, 0.6)]
+
+
+def test_identical_is_exact_and_member_swap_is_tie():
+    x, hist = _bf16_row(3)
+    p = O.RowParams(temperature=1.2, top_p=0.6, repetition_penalty=1.2, history=hist)
+    r, keep, y = _oracle(x, p, 0.3)
+    assert _kind(x, p, 0.3, keep, r.token, keep.clone(), r.token).kind == "EXACT"
+    # the cut group is kept in part: keep other members, the same number of them
+    vmin = float(y[keep].min())
+    grp = torch.nonzero(y == vmin).flatten()
+    kept = grp[keep[grp]]
+    dropped = grp[~keep[grp]]
+    assert kept.numel() > 0 and dropped.numel() > 0
+    got = keep.clone()
+    got[kept[0]] = False
+    got[dropped[0]] = True
+    v = _kind(x, p, 0.3, keep, r.token, got, None)
+    assert v.kind == "TIE", v.details
+
+
+@pytest.mark.parametrize("T,tp", WIDE)
+def test_extra_token_far_from_every_boundary(T, tp):
+    x, hist = _bf16_row(3)
+    p = O.RowParams(temperature=T, top_p=tp, repetition_penalty=1.2, history=hist)
+    r, keep, y = _oracle(x, p, 0.3)
+    got = keep.clone()
+    got[int(torch.argmin(y))] = True
+    v = _kind(x, p, 0.3, keep, r.token, got, None)
+    assert v.kind == "MISMATCH", v.details
+
+
+@pytest.mark.parametrize("T,tp", WIDE)
+def test_top_p_cut_moved_by_one_value_group_bf16(T, tp):
+    """On a 128256-value bf16 row: keeping the next value group past the cut,
+    or dropping the whole cut group, is a mistake, whatever the rounding."""
+    x, hist = _bf16_row(3)
+    p = O.RowParams(temperature=T, top_p=tp, repetition_penalty=1.2, history=hist)
+    r, keep, y = _oracle(x, p, 0.3)
+    vmin = float(y[keep].min())
+    vnext = float(y[(~keep) & (y < vmin)].max())
+    assert int((y == vnext).sum()) > 1 and int((y == vmin).sum()) > 1
+    v = _kind(x, p, 0.3, keep, r.token, keep | (y == vnext), None)
+    assert v.kind == "MISMATCH", v.details
+    v = _kind(x, p, 0.3, keep, r.token, keep & (y != vmin), None)
+    assert v.kind == "MISMATCH", v.details
+
+
+def test_top_p_cut_moved_by_one_value_group_f32():
+    x, _ = _bf16_row(3)
+    xf = x.float()     # float32 values on the bf16 grid: value groups of ~100
+    p = O.RowParams(temperature=1.5, top_p=0.9)
+    r, keep, y = _oracle(xf, p, 0.3)
+    vmin = float(y[keep].min())
+    vnext = float(y[(~keep) & (y < vmin)].max())
+    assert _kind(xf, p, 0.3, keep, r.token, keep | (y == vnext), None).kind == "MISMATCH"
+    assert _kind(xf, p, 0.3, keep, r.token, keep & (y != vmin), None).kind == "MISMATCH"
+
+
+def test_partial_group_count_outside_rounding_range():
+    """A partially kept cut group: counts inside the computed range are NEAR
+    (or TIE at the oracle's own count), counts outside it MISMATCH."""
+    x, hist = _bf16_row(3)
+    p = O.RowParams(temperature=1.0, top_p=0.95, repetition_penalty=1.2, history=hist)
+    r, keep, y = _oracle(x, p, 0.3)
+    vmin = float(y[keep].min())
+    grp = torch.nonzero(y == vmin).flatten()
+    nr = int(keep[grp].sum())
+    surv = np.ones(V, dtype=bool)
+    lo, hi, _ = C._top_p_count_range(y.double().numpy(), surv, grp.numpy(), p.top_p, torch.bfloat16)
+    assert lo <= nr <= hi
+    assert hi - lo < grp.numel()      # the doubt leaves only part of the group open
+
+    def with_count(n):
+        g = keep.clone()
+        g[grp] = False
+        g[grp[:n]] = True
+        return g
+    if lo > 0:
+        assert _kind(x, p, 0.3, keep, r.token, with_count(lo - 1), None).kind == "MISMATCH"
+    if hi < grp.numel():
+        assert _kind(x, p, 0.3, keep, r.token, with_count(hi + 1), None).kind == "MISMATCH"
+    inside = lo if lo != nr else hi
+    if inside != nr:
+        assert _kind(x, p, 0.3, keep, r.token, with_count(inside), None).kind == "NEAR"
+
+
+def test_min_p_group_far_below_threshold():
+    x, hist = _bf16_row(4)
+    p = O.RowParams(temperature=0.8, min_p=0.1, repetition_penalty=1.2, history=hist)
+    r, keep, y = _oracle(x, p, 0.5)
+    vmin = float(y[keep].min())
+    below = torch.unique(y[(~keep) & (y < vmin)])
+    vfar = float(below[len(below) // 2])     # far below the min-p cut
+    v = _kind(x, p, 0.5, keep, r.token, keep | (y == vfar), None)
+    assert v.kind == "MISMATCH", v.details
+
+
+def _mid_u(filt, tok):
+    order = O.selection_order(filt).numpy()
+    ps = torch.softmax(filt, -1).double().numpy()[order]
+    c = np.cumsum(ps) / ps.sum()
+    j = int(np.nonzero(order == tok)[0][0])
+    return float(((c[j - 1] if j else 0.0) + c[j]) / 2), order, j
+
+
+@pytest.mark.parametrize("T,tp", WIDE)
+def test_token_one_position_off_in_inverse_cdf(T, tp):
+    """The chosen token's neighbours in the selection order, at a u in the
+    middle of the chosen token's interval (tokens of probability ~1e-4)."""
+    x, hist = _bf16_row(3)
+    p = O.RowParams(temperature=T, top_p=tp, repetition_penalty=1.2, history=hist)
+    r, keep, _ = _oracle(x, p, 0.3)
+    u, order, j = _mid_u(r.filtered, r.token)
+    tok = O.select_token(r.filtered, u, T)
+    assert tok == r.token
+    for off in (-1, 1):
+        if 0 <= j + off < int(keep.sum()):
+            v = _kind(x, p, u, keep, tok, None, int(order[j + off]))
+            assert v.kind == "MISMATCH", v.details
+    # and the right token at that u is EXACT
+    assert _kind(x, p, u, keep, tok, None, tok).kind == "EXACT"
+
+
+def test_token_one_position_off_on_flat_row():
+    """Probabilities ~8e-6 each (a nearly flat 128256-value row): an
+    off-by-one pick is still far outside the rounding doubt."""
+    g = torch.Generator().manual_seed(9)
+    x = (0.01 * torch.randn(V, generator=g)).to(torch.bfloat16)
+    p = O.RowParams(temperature=1.0)
+    r, keep, _ = _oracle(x, p, 0.41)
+    u, order, j = _mid_u(r.filtered, r.token)
+    tok = O.select_token(r.filtered, u, 1.0)
+    v = _kind(x, p, u, keep, tok, None, int(order[j + 1]))
+    assert v.kind == "MISMATCH", v.details
+
+
+def test_greedy_wrong_pick_and_wrong_tie_break():
+    x, hist = _bf16_row(5)
+    p = O.RowParams(temperature=0.0)
+    r, keep, y = _oracle(x, p, 0.0)
+    order = O.selection_order(r.filtered).numpy()
+    second = [int(t) for t in order if float(y[int(t)]) < float(y[r.token])][0]
+    assert _kind(x, p, 0.0, keep, r.token, None, second).kind == "MISMATCH"
+    # a row whose maximum is shared: the first index must win
+    x2 = x.clone()
+    x2[100] = x2[50] = x.max() + 1
+    r2, keep2, _ = _oracle(x2, p, 0.0)
+    assert r2.token == 50
+    assert _kind(x2, p, 0.0, keep2, 50, None, 100).kind == "MISMATCH"
+
+
+def test_softcapped_zipf_neighbours_are_near_but_farther_is_mismatch():
+    """float32 soft-capped Zipf row (V = 262144): the token right at the top-p
+    cut lies within a part per million of top_p and is NEAR; moving the cut by
+    several tokens is not."""
+    Vz = 262144
+    g = torch.Generator().manual_seed(3)
+    ranks = torch.randperm(Vz, generator=g).float() + 1
+    x = -1.2 * torch.log(ranks) + 0.5 * torch.randn(Vz, generator=g)
+    p = O.RowParams(temperature=1.0, top_p=0.9)
+    r, keep, y = _oracle(x, p, 0.61, softcap=30.0)
+    srt = torch.sort(y, descending=True, stable=True)
+    n = int(keep.sum())
+    got = keep.clone()
+    got[srt.indices[n:n + 40]] = True
+    assert _kind(x, p, 0.61, keep, r.token, got, None, softcap=30.0).kind == "MISMATCH"
+    got = keep.clone()
+    got[srt.indices[n - 40:n]] = False
+    assert _kind(x, p, 0.61, keep, r.token, got, None, softcap=30.0).kind == "MISMATCH"
+
+
+# --------------------------------------------------------------------------
+# Speculative verify
+# --------------------------------------------------------------------------
+
+def _spec(seed=0, B=3, K=4, Vs=4096, top_k=50):
+    g = torch.Generator().manual_seed(seed)
+    z1 = torch.randn(B, K + 1, Vs, generator=g)
+    z2 = torch.randn(B, K, Vs, generator=g)
+    target = 2.0 * z1
+    draft = 2.0 * (0.8 * z1[:, :K] + 0.6 * z2)
+    p = O.RowParams(temperature=0.8, top_k=top_k, top_p=1.0)
+    ids = torch.empty(B, K, dtype=torch.int64)
+    for b in range(B):
+        for i in range(K):
+            f = O.filter_logits(draft[b, i][None], 0.8, top_k or None, None, None)[0]
+            ids[b, i] = O.select_token(f, float(torch.rand(1, generator=g)), 0.8)
+    return target, draft, ids, p, torch.rand(B, K, generator=g), torch.rand(B, generator=g)
+
+
+def test_spec_exact_on_oracle_result():
+    t, d, ids, p, ua, ur = _spec()
+    ref = O.speculative_verify(t, d, ids, p, ua, ur)
+    toks = [r.tokens + [-1] * (ids.size(1) + 1 - len(r.tokens)) for r in ref]
+    summ, _, _ = C.classify_spec(t, d, ids, p, ua, ur, [r.n_accepted for r in ref], toks, ref=ref)
+    assert summ["EXACT"] == ids.size(0)
+
+
+def test_spec_planted_mistakes():
+    t, d, ids, p, ua, ur = _spec(seed=1, B=6)
+    ref = O.speculative_verify(t, d, ids, p, ua, ur)
+    K = ids.size(1)
+    pad = lambda toks: toks + [-1] * (K + 1 - len(toks))  # noqa: E731
+    checked = 0
+    for b, r in enumerate(ref):
+        n = r.n_accepted
+        # (1) a flipped accept decision whose u is far from the ratio
+        if abs(float(ua[b, n if n < K else K - 1]) - r.accept_ratio[min(n, K - 1)]) > 1e-3:
+            if n < K:   # rejected at n: claim it was accepted
+                got_n, got_t = n + 1, r.tokens[:n] + [int(ids[b, n]), r.tokens[-1]]
+            else:       # all accepted: claim the last was rejected
+                got_n, got_t = K - 1, r.tokens[:K - 1] + [r.tokens[-1]]
+            summ, out, _ = C.classify_spec(t[b:b + 1], d[b:b + 1], ids[b:b + 1], p, ua[b:b + 1], ur[b:b + 1],
+                                           [got_n], [pad(got_t)], ref=[r])
+            assert summ["MISMATCH"] == 1, out
+            checked += 1
+        # (2) the resampled / bonus token one position off
+        last = r.tokens[-1]
+        if n < K:
+            pt, _ = O.filtered_probs(t[b, n], p)
+            pd, _ = O.filtered_probs(d[b, n], p)
+            rr = torch.clamp(pt - pd, min=0).double()
+            nz = torch.nonzero(rr > 0).flatten().tolist()
+            k = nz.index(last) if last in nz else None
+            wrong = nz[k + 1] if k is not None and k + 1 < len(nz) else None
+        else:
+            _, filt = O.filtered_probs(t[b, K], p)
+            order = O.selection_order(filt).tolist()
+            k = order.index(last)
+            wrong = order[k + 1] if torch.isfinite(filt[order[k + 1]]) else order[k - 1]
+        if wrong is not None:
+            summ, out, _ = C.classify_spec(t[b:b + 1], d[b:b + 1], ids[b:b + 1], p, ua[b:b + 1], ur[b:b + 1],
+                                           [n], [pad(r.tokens[:-1] + [wrong])], ref=[r])
+            assert summ["MISMATCH"] == 1, out
+            checked += 1
+    assert checked >= 6

@@ -44,7 +44,39 @@ def test_batched_sampler_matches_per_request_loop():
                 v = C.classify_row(x[b], rp, float(u[b]), keep, ref.token, None, toks[b])
                 assert v.ok, (step, b, toks[b], ref.token, v.details[:3])
             assert fins[b] == ref.finished, (step, b)
-            hist[b].append(toks[b])
+            if not finished[b]:       # a finished request is retired: nothing more joins its history
+                hist[b].append(toks[b])
             finished[b] = fins[b]
     for b in range(B):
         assert bs.history_of(b) == hist[b]
+
+
+def test_batched_sampler_slots_release_and_state_in_place():
+    """Rows mapped to slots by index (a decode group without the retired
+    sequences), a released slot that appends nothing, and the same results as
+    the positional call on the same state."""
+    V = 4096
+    p = SamplingParams(temperature=0.9, top_k=40, repetition_penalty=1.2)
+    a = BatchedSampler(6, 64, V, "cuda", eos_token_id=1)
+    b = BatchedSampler(6, 64, V, "cuda", eos_token_id=1)
+    for s in range(6):
+        a.admit(s, p, [10 + s, 20 + s])
+        b.admit(s, p, [10 + s, 20 + s])
+    a.release(2)
+    g = torch.Generator().manual_seed(3)
+    for _ in range(5):
+        x = (torch.randn(6, V, generator=g) * 2.0).cuda()
+        u = torch.rand(6, generator=g).cuda()
+        # b: the full group by position; a: slots 5, 0, 3 only, in that order
+        ob = b.step(x, uniforms=u)
+        sel = torch.tensor([5, 0, 3], device="cuda")
+        oa = a.step(x[sel], uniforms=u[sel].contiguous(), slots=sel)
+        assert oa.tokens.tolist() == ob.tokens[sel].tolist()
+    for s in (0, 3, 5):
+        assert a.history_of(s) == b.history_of(s)
+    assert a.history_of(2) == []                   # released: emptied, nothing appended
+    assert a.history_of(1) == [11, 21]             # not in the group: untouched
+    assert bool(a.finished[2])
+    ptr = a.history.data_ptr()
+    a.step(torch.randn(6, V, device="cuda"), uniforms=torch.rand(6, device="cuda"))
+    assert a.history.data_ptr() == ptr

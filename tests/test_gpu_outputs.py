@@ -121,7 +121,12 @@ def test_outputs_match_oracle(name):
             rp32 = rp.float()
             err = (probs[b] - rp32).abs()
             assert bool((err <= 1e-2 * rp32.abs() + 1.2e-38).all()), (b, float(err.max()))
-            assert abs(float(lps[b]) - ref[b].logprob) <= 2e-2 * max(1.0, abs(ref[b].logprob)), b
+            # torch's 16-bit log_softmax rounds the mass and its log to the
+            # dtype; the kernel does the same: equal up to one unit
+            lref = torch.tensor([ref[b].logprob], dtype=torch.float32).to(rf.dtype)
+            unit = float((lref.view(torch.int16) + 1).view(rf.dtype).double() - lref.double()) if lref.item() != 0 \
+                else 0.0
+            assert abs(float(lps[b]) - ref[b].logprob) <= abs(unit), (b, float(lps[b]), ref[b].logprob)
         assert bool(fins[b]) == ref[b].finished, (b, bool(fins[b]), ref[b].finished)
     # the rows that arrived finished stay finished whatever they sample
     assert all(bool(fins[r]) for r in fin_rows)
