@@ -75,15 +75,16 @@ def _isolated_launches(torch, dev, stream, launch, n: int = ISOLATED):
     return sorted(a.elapsed_time(b) for a, b in ev)
 
 
-def cpu_baseline(w, seconds: float, got_tokens=None):
+def cpu_baseline(w, seconds: float, got_tokens=None, got_mask=None):
     """The oracle's per-row restatement (one [1, V] call per row, as the
     reference inference engine makes them) on the first rows of the workload:
     the median rate of three segments of ``seconds / 3`` with all the threads
     torch uses, and one segment of ``seconds / 3`` on a single thread.
 
-    ``got_tokens`` (the GPU's tokens for the same batch): the oracle tokens of
-    the rows the baseline sampled are checked against them, outside the timed
-    segments, and the counts are returned under ``parity``."""
+    ``got_tokens`` / ``got_mask`` (the GPU's tokens and keep bit-masks for the
+    same batch): the oracle tokens of the rows the baseline sampled are
+    checked against them, outside the timed segments, and the counts are
+    returned under ``parity``."""
     import statistics
 
     import torch
@@ -125,7 +126,7 @@ def cpu_baseline(w, seconds: float, got_tokens=None):
         torch.set_num_threads(threads)
     parity = None
     if got_tokens is not None:
-        parity = _row_parity(w, x, params, u, oracle_tok, got_tokens)
+        parity = _row_parity(w, x, params, u, oracle_tok, got_tokens, got_mask)
     return {"value": statistics.median(rates), "unit": "rows/s", "cores": threads, "kind": "port",
             "single_thread_value": one, "parity": parity,
             "sample": f"{state['row']} rows of {w.name} (seed 0, cycling through its {w.batch} rows), one [1,V] "
@@ -135,16 +136,17 @@ def cpu_baseline(w, seconds: float, got_tokens=None):
                       f"single_thread_value: one segment of {seconds / 3:.1f} s on 1 thread"}
 
 
-def _row_parity(w, x, params, u, oracle_tok, got_tokens):
+def _row_parity(w, x, params, u, oracle_tok, got_tokens, got_mask=None):
     """EXACT / TIE / NEAR / CONSEQ / MISMATCH counts of the GPU tokens of the
     rows the CPU baseline sampled, against its oracle tokens (a differing
-    token is classified with the oracle's keep mask and rounding doubt)."""
+    token is classified with both keep masks and the rounding doubt)."""
     import torch
 
     from oracle import classify as C
     from oracle import sampler_oracle as O
 
     got = got_tokens.cpu().tolist()
+    words = None if got_mask is None else got_mask.cpu().to(torch.int64) & 0xFFFFFFFF
     counts = {k: 0 for k in ("EXACT", "TIE", "NEAR", "CONSEQ", "MISMATCH")}
     for b, tok in sorted(oracle_tok.items()):
         if got[b] == tok:
@@ -152,7 +154,10 @@ def _row_parity(w, x, params, u, oracle_tok, got_tokens):
             continue
         ref = O.sample_rows(x[b:b + 1], params[b:b + 1], u[b:b + 1], softcap=w.softcap)[0]
         keep = ~torch.isneginf(ref.filtered.float())
-        v = C.classify_row(x[b], params[b], u[b], keep, ref.token, None, got[b], softcap=w.softcap)
+        gk = None
+        if words is not None:
+            gk = (((words[b].unsqueeze(-1) >> torch.arange(32)) & 1).reshape(-1)[:w.vocab]).bool()
+        v = C.classify_row(x[b], params[b], u[b], keep, ref.token, gk, got[b], softcap=w.softcap)
         counts[v.kind] += 1
     counts["rows_checked"] = len(oracle_tok)
     counts["batch_rows"] = w.batch
@@ -435,9 +440,13 @@ def main() -> int:
                      "kernel": "k_sample_rows16<BF16, false>" if w.logits.element_size() == 2 else "k_sample_rows32"},
     }
     if not args.no_cpu_baseline:
-        plans[0].launch()      # the first batch's own tokens, checked against the oracle
+        from rl_project_amd import filtered_outputs
+        plans[0].launch()      # the first batch's own tokens and keep masks, checked against the oracle
+        kw_mask = dict(kw)
+        kw_mask.pop("uniforms")
+        _, _, mask0, _ = filtered_outputs(bufs[0], want_filtered=False, want_mask=True, **kw_mask)
         torch.cuda.synchronize(dev)
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, plans[0].output.tokens.clone())
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, plans[0].output.tokens.clone(), mask0)
         result["parity"] = result["cpu_baseline"]["parity"]
     print(json.dumps(result), flush=True)
     return 0

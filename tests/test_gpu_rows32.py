@@ -105,3 +105,19 @@ def test_param_edges_f32(case):
         kw["top_k"] = torch.ones(B, dtype=torch.int32)
     print(f"[param edges f32] {case} B={B} V={V}", flush=True)
     _check(_with(w, **kw))
+
+
+def test_f32_greedy_first_index_among_equal_probabilities():
+    """torch.argmax(softmax(x)) (sampling.py:58-60) compares float32
+    probabilities: values a few ulp apart near zero share the maximum's
+    probability and the first index wins."""
+    import numpy as np
+    a = np.float32(0.1)
+    b = np.nextafter(a, np.float32(1.0))
+    rows = torch.tensor([[a, b, -3.0], [b, a, -3.0], [-3.0, a, b], [5.0, np.nextafter(np.float32(5.0), np.float32(9.0)), 0.0]],
+                        dtype=torch.float32)
+    x = torch.nn.functional.pad(rows, (0, 61), value=-30.0)
+    out = sample_tokens(x.cuda(), temperature=0.0, uniforms=torch.zeros(4, device="cuda"))
+    want = [int(torch.argmax(torch.softmax(x[i], -1))) for i in range(4)]
+    assert want[:3] == [0, 0, 1] and want[3] == 1
+    assert out.tokens.tolist() == want

@@ -54,7 +54,11 @@ def test_spec_plan_reads_uniforms_in_place():
         ua2 = torch.rand(B, 5, generator=g).cuda()
         ur2 = torch.rand(B, generator=g).cuda()
         if step == 2:
-            ua2.fill_(0.0)          # every draft accepted: the bonus draw decides
+            # drafts equal to the target's top token (p == q): every draft is
+            # accepted and the bonus draw decides
+            draft.copy_(target[:, :5])
+            ids.copy_(target[:, :5].argmax(-1))
+            ua2.fill_(0.0)
         plan.u_accept.copy_(ua2)
         plan.u_resample.copy_(ur2)
         plan.launch()

@@ -478,3 +478,12 @@ def test_scalar_products_of_16_bit_tensors_use_float32_scalars():
             assert not torch.equal(as_f32, as_dt)   # the two readings do differ
     b = torch.tensor([0.94921875, 0.953125], dtype=torch.bfloat16)
     assert (b >= 0.95).tolist() == [True, True]     # 0.95 compares as bf16 0.94921875
+
+
+def test_greedy_compares_float32_probabilities():
+    """T <= 0 is torch.argmax of the float32 probabilities: logits one ulp
+    apart near zero have equal probabilities and the first index wins."""
+    a = np.float32(0.1)
+    row = torch.tensor([a, np.nextafter(a, np.float32(1.0)), -3.0], dtype=torch.float32)
+    assert O.select_token(row, 0.5, 0.0) == 0
+    assert int(torch.argmax(row)) == 1
