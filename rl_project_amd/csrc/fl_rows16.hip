@@ -158,27 +158,27 @@ __device__ __forceinline__ uint32_t penalised_bits(uint32_t z, float rp) {
 }
 // filtered value of a pattern given as an order index (soft-cap if `sc`)
 template <class D>
-__device__ __noinline__ float value_of_order(uint32_t order, float cap, float t, bool sc) {
+__device__ __noinline__ float value_of_order(uint32_t order, float cap, float t, float rt, bool sc) {
   float z = D::to_f32(bits_of_order16(order));
   if (sc) z = softcap_val<D>(z, cap);
-  return temperature_val<D>(z, t);
+  return temperature_val<D>(z, t, rt);
 }
 template <class D>
-__device__ __noinline__ float e_of_order(uint32_t order, float cap, float t, bool sc, float M) {
-  return expf(value_of_order<D>(order, cap, t, sc) - M);
+__device__ __noinline__ float e_of_order(uint32_t order, float cap, float t, float rt, bool sc, float M) {
+  return expf(value_of_order<D>(order, cap, t, rt, sc) - M);
 }
 // The same for a kernel instantiated with or without the soft-cap: without
 // it the value is cheap and inline, and the kernel makes no calls (a call
 // would keep most VGPRs from holding values across it).
 template <class D, bool SC>
-__device__ __forceinline__ float y_of_order(uint32_t order, float cap, float t, bool sc) {
-  if constexpr (SC) return value_of_order<D>(order, cap, t, sc);
-  else return temperature_val<D>(D::to_f32(bits_of_order16(order)), t);
+__device__ __forceinline__ float y_of_order(uint32_t order, float cap, float t, float rt, bool sc) {
+  if constexpr (SC) return value_of_order<D>(order, cap, t, rt, sc);
+  else return temperature_val<D>(D::to_f32(bits_of_order16(order)), t, rt);
 }
 template <class D, bool SC>
-__device__ __forceinline__ float exp_of_order(uint32_t order, float cap, float t, bool sc, float M) {
-  if constexpr (SC) return e_of_order<D>(order, cap, t, sc, M);
-  else return expf(y_of_order<D, false>(order, cap, t, false) - M);
+__device__ __forceinline__ float exp_of_order(uint32_t order, float cap, float t, float rt, bool sc, float M) {
+  if constexpr (SC) return e_of_order<D>(order, cap, t, rt, sc, M);
+  else return expf(y_of_order<D, false>(order, cap, t, rt, false) - M);
 }
 
 }  // namespace
@@ -282,6 +282,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // u outside [0, 1) (or NaN) is clamped into it
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const float CAP = a.softcap;
+  const float RT = T > 0.0f ? 1.0f / T : 0.0f;  // one IEEE division per row (temperature_val)
   // (H_in is only meaningful with a history: without one it was read from the stand-in array)
   const bool hist_too_long = a.hist_ids != nullptr && H_in > FL_MAX_HISTORY;
   // (the history bitmap covers TILE_V values: a longer row is penalised nowhere)
@@ -534,7 +535,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const int lo = min(N, tid * per), hi = min(N, lo + per);
 
   auto cnt_of = [&](int i) -> uint32_t { return entry_count(ent[i]); };
-  auto y_raw = [&](int i) -> float { return y_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry); };
+  auto y_raw = [&](int i) -> float { return y_of_order<D, SC>(ent[i] >> 16, CAP, T, RT, sc_entry); };
   const float M = N > 0 ? y_raw(0) : 0.0f;
   // -inf values of the row (read where a total is off or nothing is left)
   auto neg_inf_count = [&]() -> uint32_t {
@@ -548,13 +549,13 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     else if (isinf(M)) sh.status |= (M > 0.0f) ? FL_ROW_INF : FL_ROW_ALL_MASKED;
   }
   auto Y = [&](int i) -> float { return cached ? Yc[i] : y_raw(i); };
-  auto E = [&](int i) -> float { return cached ? Ec[i] : exp_of_order<D, SC>(ent[i] >> 16, CAP, T, sc_entry, M); };
+  auto E = [&](int i) -> float { return cached ? Ec[i] : exp_of_order<D, SC>(ent[i] >> 16, CAP, T, RT, sc_entry, M); };
   {
     uint32_t lc = 0;
     uint64_t lm = 0;
     for (int i = lo; i < hi; ++i) {
       const uint32_t en = ent[i];
-      const float y = y_of_order<D, SC>(en >> 16, CAP, T, sc_entry);
+      const float y = y_of_order<D, SC>(en >> 16, CAP, T, RT, sc_entry);
       const float e = expf(y - M);
       if (cached) {
         Yc[i] = y;

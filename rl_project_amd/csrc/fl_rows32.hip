@@ -157,7 +157,7 @@ struct Src {
 // Logit -> filtered value: soft-cap, repetition penalty (history elements),
 // temperature, each rounded to float32 as the reference's tensor ops round.
 struct Xform {
-  float cap, rp, t;
+  float cap, rp, t, rt;  // rt = RN(1 / t) when t > 0
   bool pen;
   const uint32_t* hbits;
   int nch;
@@ -166,7 +166,7 @@ struct Xform {
     if (cap > 0.0f) z = softcap_val<F32>(z, cap);
     if (hist) z = penalty_val<F32>(z, rp);
     // + 0.0f turns -0 into +0: the filters compare -0 == +0, so both get one key
-    return temperature_val<F32>(z, t) + 0.0f;
+    return temperature_val<F32>(z, t, rt) + 0.0f;
   }
   // y with the row's uniform choices fixed at compile time: TDIV = t > 0
   // (a division by the temperature), PEN = pen.  Equal to y() bit for bit.
@@ -175,7 +175,7 @@ struct Xform {
     float z = x;
     if (cap > 0.0f) z = softcap_val<F32>(z, cap);
     if (PEN && hist) z = penalty_val<F32>(z, rp);
-    if (TDIV) z = F32::rn(z / t);
+    if (TDIV) z = div_rt(z, t, rt);
     return z + 0.0f;
   }
   // history bits of elements 4c .. 4c+3
@@ -1030,6 +1030,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   X.cap = a.softcap;
   X.rp = RP;
   X.t = T == 1.0f ? 0.0f : T;  // x / 1 == x exactly: skip the division
+  X.rt = X.t > 0.0f ? 1.0f / X.t : 0.0f;
   X.pen = pen;
   X.hbits = hbits_dyn;
   X.nch = nch;
