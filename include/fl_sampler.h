@@ -58,7 +58,7 @@ enum fl_row_status {
 
 /* Limits of the library. */
 #define FL_MAX_VOCAB_F32 262144     /* fp32 rows                       */
-#define FL_MAX_VOCAB_16  262144     /* bf16 / fp16 rows (repetition penalty: 131072) */
+#define FL_MAX_VOCAB_16  262144     /* bf16 / fp16 rows                */
 #define FL_MAX_HISTORY   65536      /* history ids per row             */
 
 /*
@@ -108,6 +108,15 @@ typedef struct fl_row_desc {
  * be writable device memory.  The decode-loop bookkeeping of the reference
  * engine (engine.py:122, the generated id joins the request's tokens) in the
  * same launch.
+ * bf16 / fp16 rows in which one value fills more than 65535 positions (an
+ * all-zero row, a mask with a finite floor such as finfo.min) exceed the
+ * 16-bit value counters of the default kernel and report FL_ROW_LIMIT;
+ * FL_FLAG_EXACT_COUNTS samples any row with 32-bit counts of such values
+ * (slower; the same results on every other row).  Adding
+ * FL_FLAG_ONLY_LIMITED repeats a call for the rows whose out_status it left
+ * at FL_ROW_LIMIT and leaves every other row's outputs as they are (no host
+ * synchronisation needed: the kernel reads out_status).  The Python binding
+ * makes that repeat after a call that reports FL_ROW_LIMIT.
  */
 typedef struct fl_sample_args {
   uint32_t struct_size;        /* sizeof(fl_sample_args) */
@@ -141,6 +150,8 @@ typedef struct fl_sample_args {
 
 #define FL_FLAG_NO_SELECT 1       /* describe the filtered distribution only */
 #define FL_FLAG_APPEND_HISTORY 2  /* append each sampled token to its row's history */
+#define FL_FLAG_EXACT_COUNTS 4    /* bf16 / fp16: count values exactly (see below) */
+#define FL_FLAG_ONLY_LIMITED 8    /* with EXACT_COUNTS: only rows whose out_status holds FL_ROW_LIMIT */
 
 /*
  * Batched sample: replaces the per-request loop

@@ -22,6 +22,8 @@ FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
 FL_FLAG_NO_SELECT = 1
 FL_FLAG_APPEND_HISTORY = 2
+FL_FLAG_EXACT_COUNTS = 4
+FL_FLAG_ONLY_LIMITED = 8
 FL_MAX_VOCAB_F32 = 262144
 FL_MAX_VOCAB_16 = 262144
 FL_MAX_HISTORY = 65536

@@ -53,8 +53,10 @@ int validate_sample(const fl_sample_args* a, const char* fn) {
     return fail(FL_EINVAL, "%s: hist_ids needs hist_len and hist_ld >= 0", fn);
   if (a->n_stop < 0 || (a->n_stop > 0 && (a->stop_ids == nullptr || a->stop_ld < 0)))
     return fail(FL_EINVAL, "%s: stop_ids/n_stop/stop_ld inconsistent", fn);
-  if ((a->flags & ~(FL_FLAG_NO_SELECT | FL_FLAG_APPEND_HISTORY)) != 0)
+  if ((a->flags & ~(FL_FLAG_NO_SELECT | FL_FLAG_APPEND_HISTORY | FL_FLAG_EXACT_COUNTS | FL_FLAG_ONLY_LIMITED)) != 0)
     return fail(FL_EINVAL, "%s: unknown flags 0x%x", fn, static_cast<unsigned>(a->flags));
+  if ((a->flags & FL_FLAG_ONLY_LIMITED) && (!(a->flags & FL_FLAG_EXACT_COUNTS) || a->out_status == nullptr))
+    return fail(FL_EINVAL, "%s: FL_FLAG_ONLY_LIMITED needs FL_FLAG_EXACT_COUNTS and out_status", fn);
   if (a->uniform_div < 0) return fail(FL_EINVAL, "%s: uniform_div %lld < 0", fn, static_cast<long long>(a->uniform_div));
   if ((a->flags & FL_FLAG_APPEND_HISTORY) &&
       (a->hist_ids == nullptr || a->hist_ld <= 0 || (a->flags & FL_FLAG_NO_SELECT)))
@@ -82,6 +84,8 @@ int fl_sample(const fl_sample_args* a, void* stream) {
   if (select && a->batch > 0 && a->uniforms == nullptr)
     return fail(FL_EINVAL, "fl_sample: uniforms is NULL (one draw per row is required unless FL_FLAG_NO_SELECT)");
   if (a->batch == 0) return ok();
+  // (float32 rows have no 16-bit counters: a repeat for limited rows has nothing to do)
+  if (a->dtype == FL_DTYPE_F32 && (a->flags & FL_FLAG_ONLY_LIMITED)) return ok();
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = a->dtype == FL_DTYPE_F32 ? fl::launch_sample_rows32(*a, s) : fl::launch_sample_rows16(*a, s);
   return check_launch(e, "fl_sample");

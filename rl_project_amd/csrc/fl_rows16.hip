@@ -20,6 +20,8 @@
 //
 // Order convention: descending filtered value, ties by ascending vocabulary
 // index.  All sums are float64 in a fixed order, so results are deterministic.
+#include <type_traits>
+
 #include "fl_device.h"
 #include "fl_kernels.h"
 
@@ -41,6 +43,7 @@ constexpr int NSTEP = 512;                        // compaction steps of 128 ord
 constexpr int SPW = NSTEP / NWAVE;                // steps per wave
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 constexpr int EARLY_CHUNKS = 2;                  // row chunks per thread requested before the LDS clear
+constexpr int MAX_HEAVY = 8;                     // patterns with more than 65535 values (at most 5 exist)
 
 static_assert(NSLOT * NT * 8 == FL_MAX_VOCAB_16 && NSLOT >= NCH, "identification slots cover the longest row");
 
@@ -66,6 +69,10 @@ struct Shared16 {
   uint32_t wc[2][NSLOT][NWAVE];  // identification: members per slot of NT chunks and wave
   uint32_t nh[2];         // identification: history members
   uint32_t inf_extra;     // soft-capped rows: -inf values beyond their pattern's 16-bit count
+  // patterns with more than 65535 values (at most 5: V + unique history ids
+  // <= 327680): their order, exact count and the part beyond the 16-bit field
+  uint32_t n_heavy;
+  uint32_t hv_order[MAX_HEAVY], hv_count[MAX_HEAVY], hv_extra[MAX_HEAVY];
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -181,21 +188,140 @@ __device__ __forceinline__ float exp_of_order(uint32_t order, float cap, float t
   else return expf(y_of_order<D, false>(order, cap, t, rt, false) - M);
 }
 
+// ------------------------------------------------ more than 65535 equal values
+// A 16-bit counter wraps past 65535 (a constant or all-zero row, a mask with
+// a finite floor such as finfo.min): the compaction then sees fewer values
+// than the row holds.  Such a row recounts exactly (a few microseconds):
+//   1. 32-bit counts of each half of the orders in the histogram's memory:
+//      the values plus the ids the penalty moves in (a pattern whose count can
+//      pass 65535 at any time of the counting is flagged), then less the ids
+//      moved out (the flagged patterns' final counts);
+//   2. the 16-bit histogram rebuilt without the flagged patterns, which get
+//      as much of their count as 16 bits hold; the rest is kept per pattern
+//      (hv_extra) and added wherever an entry's count is read.
+// It does all the counting of the recounting body: the -inf values go to
+// their lanes' counters as in the first count.
+template <class D>
+__device__ __forceinline__ void heavy_recount(Shared16& sh, const uint16_t* row, int V, int nfull, bool aligned,
+                                           bool sc_elem, float cap, const int32_t* hid, int H, bool pen, float rp) {
+  const int tid = threadIdx.x;
+  constexpr uint32_t NEG_INF_RAW = 0x8000u | D::INF_BITS;
+  auto elem_bits = [&](uint32_t raw) -> uint32_t { return sc_elem ? capped_bits<D>(raw, cap) : raw; };
+  const bool neg_inf_value = cap > 0.0f;  // -inf is a value (-cap) only under a soft-cap
+  auto for_each_value = [&](auto&& f) {  // f(raw) for every element
+    for (int c = tid; c < nfull; c += NT) {
+      const uint4 q = load_chunk16(row, c, V, aligned);
+      const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
+    }
+    if (tid == 0)
+      for (int i = nfull * 8; i < V; ++i) f(static_cast<uint32_t>(row[i]));
+  };
+  auto for_each_unique_id = [&](auto&& f) {  // f(raw) for the logit of every unique history id
+    if (!pen) return;
+    for (int i = tid; i < H; i += NT)
+      if ((sh.owner[i >> 5] >> (i & 31)) & 1u) f(static_cast<uint32_t>(row[hid[i]]));
+  };
+  auto is_heavy = [&](uint32_t bits) {
+    const uint32_t o = order16(bits);
+    bool h = false;
+    for (uint32_t k = 0; k < sh.n_heavy; ++k) h |= sh.hv_order[k] == o;
+    return h;
+  };
+  uint32_t* c32 = sh.hist;  // 32768 counters: orders 32768 h .. 32768 h + 32767
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(c32)[tid + k * NT] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    auto add_if = [&](uint32_t bits, uint32_t v) {
+      const uint32_t o = order16(bits);
+      if ((o >> 15) == static_cast<uint32_t>(h)) atomicAdd(&c32[o & 0x7FFFu], v);
+    };
+    for_each_value([&](uint32_t raw) {
+      // (a soft-capped row's -inf values are counted under the pattern the
+      // -inf counters join: elem_bits(-inf))
+      if (raw != NEG_INF_RAW || neg_inf_value) add_if(elem_bits(raw), 1u);
+    });
+    for_each_unique_id([&](uint32_t raw) {
+      const uint32_t z = elem_bits(raw), zp = penalised_bits<D>(z, rp);
+      if (zp != z) add_if(zp, 1u);
+    });
+    __syncthreads();
+    for (int k = 0; k < 32; ++k) {
+      const int i = tid * 32 + ((k + tid) & 31);  // (staggered: no bank conflicts)
+      if (c32[i] > 0xFFFFu) {
+        const uint32_t slot = atomicAdd(&sh.n_heavy, 1u);
+        if (slot < static_cast<uint32_t>(MAX_HEAVY)) sh.hv_order[slot] = 32768u * h + static_cast<uint32_t>(i);
+      }
+    }
+    __syncthreads();
+    for_each_unique_id([&](uint32_t raw) {
+      const uint32_t z = elem_bits(raw), zp = penalised_bits<D>(z, rp);
+      if (zp != z) add_if(z, 0xFFFFFFFFu);
+    });
+    __syncthreads();
+    if (tid < static_cast<int>(min(sh.n_heavy, static_cast<uint32_t>(MAX_HEAVY))) &&
+        (sh.hv_order[tid] >> 15) == static_cast<uint32_t>(h))
+      sh.hv_count[tid] = c32[sh.hv_order[tid] & 0x7FFFu];
+  }
+  __syncthreads();
+  if (tid == 0 && sh.n_heavy > static_cast<uint32_t>(MAX_HEAVY)) {  // cannot happen (at most 5 exist)
+    sh.n_heavy = MAX_HEAVY;
+    atomicOr(&sh.status, FL_ROW_LIMIT);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) reinterpret_cast<uint4*>(sh.hist)[tid + k * NT] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  for_each_value([&](uint32_t raw) {
+    if (raw == NEG_INF_RAW) {  // the -inf values in this lane's counter past the patterns
+      atomicAdd(&sh.hist[HIST_WORDS + (tid & (WAVE - 1))], 1u);
+      return;
+    }
+    const uint32_t bits = elem_bits(raw);
+    if (!is_heavy(bits)) atomicAdd(&sh.hist[bits >> 1], 1u + (bits & 1u) * 0xFFFFu);
+  });
+  __syncthreads();
+  for_each_unique_id([&](uint32_t raw) {
+    const uint32_t z = elem_bits(raw), zp = penalised_bits<D>(z, rp);
+    if (zp == z) return;
+    // (a soft-capped raw -inf leaves its lane's -inf counter)
+    if (neg_inf_value && raw == NEG_INF_RAW) atomicAdd(&sh.hist[HIST_WORDS + (tid & (WAVE - 1))], 0xFFFFFFFFu);
+    else if (!is_heavy(z)) atomicAdd(&sh.hist[z >> 1], (z & 1u) ? 0xFFFF0000u : 0xFFFFFFFFu);
+    if (!is_heavy(zp)) atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
+  });
+  __syncthreads();
+  if (tid < static_cast<int>(sh.n_heavy)) {
+    const uint32_t P = bits_of_order16(sh.hv_order[tid]);
+    const uint32_t c = sh.hv_count[tid], f = min(c, 0xFFFFu);
+    atomicAdd(&sh.hist[P >> 1], (P & 1u) ? (f << 16) : f);
+    sh.hv_extra[tid] = c - f;
+  }
+  __syncthreads();
+}
+
 }  // namespace
 
 // SC: the row has a soft-cap (applied per element when SC_ELEM, else per
 // entry).  The instantiation without it keeps the first read's VGPR tile for
 // the identification; the one with it reads the row again.
-template <class D, bool SC>
-__global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN) {
-  __shared__ Shared16 sh;
+// HEAVY: the exact-count body -- no register tile, the histogram counted by
+// heavy_recount, counts beyond 16 bits kept per pattern.
+template <class D, bool SC, bool HEAVY>
+__device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN,
+                                         Shared16& sh) {
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
+  // (a repeat for the rows a first call left at FL_ROW_LIMIT: the others keep
+  // their outputs; block-uniform, before any barrier)
+  if constexpr (HEAVY)
+    if ((a.flags & FL_FLAG_ONLY_LIMITED) && (a.out_status[b] & FL_ROW_LIMIT) == 0) return true;
   const int V = static_cast<int>(a.vocab);
   const uint16_t* row = static_cast<const uint16_t*>(a.logits) + b * a.ld;
   const bool SC_ELEM = SC && SC_ELEM_IN;
   const int nfull = V >> 3;                               // chunks holding 8 valid elements
-  const bool fast = ALIGNED && !SC_ELEM && nfull > 0 && V <= TILE_V;  // whole row through the VGPR tile
+  const bool fast_row = !HEAVY && ALIGNED && !SC_ELEM && nfull > 0 && V <= TILE_V;  // whole row through the VGPR tile
 
   // ------------------------------------------------ loads
   // Issue order matters: the per-row parameters (scalar loads) first, so they
@@ -229,7 +355,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // the clear's barrier: a wave stalls in issuing its loads until the memory
   // system accepts them (at the HBM rate), so a barrier placed after all of
   // them would only open once most of the row had arrived.
-  const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast ? 2u * static_cast<uint32_t>(V) : 0u);
+  const __amdgpu_buffer_rsrc_t rrow = row_rsrc(row, fast_row ? 2u * static_cast<uint32_t>(V) : 0u);
   uint4 d[NCH];
 #pragma unroll
   for (int j = 0; j < EARLY_CHUNKS; ++j) {
@@ -251,6 +377,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   if (tid == 0) {
     sh.status = 0;
     sh.nh[0] = sh.nh[1] = 0;
+    sh.n_heavy = 0;
     sh.result[0] = sh.result[1] = -1;
     sh.dec.L = 0;
     sh.dec.i0 = -1;
@@ -285,12 +412,14 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   const float RT = T > 0.0f ? 1.0f / T : 0.0f;  // one IEEE division per row (temperature_val)
   // (H_in is only meaningful with a history: without one it was read from the stand-in array)
   const bool hist_too_long = a.hist_ids != nullptr && H_in > FL_MAX_HISTORY;
-  // (the history bitmap covers TILE_V values: a longer row is penalised nowhere)
-  const bool pen_too_wide = a.hist_ids != nullptr && RP != 1.0f && H_in > 0 && V > TILE_V;
-  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long && !pen_too_wide) ? max(H_in, 0) : 0;
+  const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
+  // Rows longer than the history bitmap (TILE_V values) de-duplicate their
+  // history in two windows of TILE_V ids and keep the full bitmap in the
+  // histogram's memory for the identification.
+  const bool wide = V > TILE_V;
   const bool sc_entry = SC && (CAP > 0.0f) && !SC_ELEM;
-  if (tid == 0 && (hist_too_long || pen_too_wide)) atomicOr(&sh.status, FL_ROW_LIMIT);
+  if (tid == 0 && hist_too_long) atomicOr(&sh.status, FL_ROW_LIMIT);
 
   // Value pattern of an element as the filters see it before penalty.
   auto elem_bits = [&](uint32_t raw) -> uint32_t {
@@ -302,21 +431,24 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   // load overlaps the counting pass below.
   uint32_t xh[HPRE];
   bool own[HPRE];
-  auto claim = [&](int i, int id) -> bool {
+  // (window w of a wide row: ids w * TILE_V .. w * TILE_V + TILE_V - 1)
+  auto claim = [&](int i, int id, int w) -> bool {
     if (id < 0 || id >= V) {
-      atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
+      if (w == 0) atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
       return false;
     }
-    const uint32_t bit = 1u << (id & 31);
-    if (atomicOr(&sh.hbits[id >> 5], bit) & bit) return false;  // a duplicate id
+    const int bid = id - w * TILE_V;
+    if (static_cast<uint32_t>(bid) >= static_cast<uint32_t>(TILE_V)) return false;  // the other window
+    const uint32_t bit = 1u << (bid & 31);
+    if (atomicOr(&sh.hbits[bid >> 5], bit) & bit) return false;  // a duplicate id
     atomicOr(&sh.owner[i >> 5], 1u << (i & 31));
     return true;
   };
 #pragma unroll
   for (int k = 0; k < HPRE; ++k) {
     const int i = tid + k * NT;
-    own[k] = pen && hist_rows && i < H;
-    if (own[k]) own[k] = claim(i, hpre[k]);
+    own[k] = !HEAVY && pen && hist_rows && i < H && !wide;
+    if (own[k]) own[k] = claim(i, hpre[k], 0);
   }
 #pragma unroll
   for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
@@ -340,7 +472,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       atomicAdd(&sh.hist[raw == NEG_INF_RAW ? inf_word : raw >> 1], 1u + (raw & 1u) * 0xFFFFu);
     }
   };
-  if (fast) {
+  if constexpr (!HEAVY) {  // (the recounting body counts in heavy_recount)
+  if (fast_row) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       if (j * NT + tid < nfull) {
@@ -359,6 +492,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   }
   if (tid == 0)
     for (int i = nfull * 8; i < V; ++i) count(row[i]);
+  }
 
   FL_MARK(12);
   // ------------------------------------------------ repetition penalty
@@ -376,35 +510,59 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 #pragma unroll
   for (int k = 0; k < HPRE; ++k)
     if (own[k]) penalise(xh[k]);
-  for (int i = tid + (hist_rows ? HPRE * NT : 0); i < H; i += NT) {
-    const int id = hid[i];
-    if (claim(i, id)) penalise(row[id]);
+  if (!wide) {
+    for (int i = tid + ((hist_rows && !HEAVY) ? HPRE * NT : 0); i < H; i += NT) {
+      const int id = hid[i];
+      if (claim(i, id, 0) && !HEAVY) penalise(row[id]);
+    }
+  } else if (pen) {
+    for (int w = 0; w < 2; ++w) {
+      if (w == 1) {  // the second window's ids through a cleared bitmap
+        __syncthreads();
+        reinterpret_cast<uint4*>(sh.hbits)[tid] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+      }
+      for (int i = tid; i < H; i += NT) {
+        const int id = hid[i];
+        if (claim(i, id, w) && !HEAVY) penalise(row[id]);
+      }
+    }
   }
   __syncthreads();
   // soft-capped rows: the -inf values join the count of their pattern (that of
-  // -cap), as far as its 16 bits hold
+  // -cap), as far as its 16 bits hold (not at all where -cap is a pattern of
+  // more than 65535 values, whose count is exact and includes them)
   uint32_t inf_extra = 0, inf_order = 0xFFFFFFFFu;
-  if constexpr (SC) {
-    if (tid < WAVE) {
-      const uint32_t nin = wave_reduce(sh.hist[HIST_WORDS + tid], OpAdd{});
-      if (tid == 0) {
-        uint32_t add = 0;
-        if (nin != 0u) {
+  auto merge_neg_inf = [&]() {
+    if constexpr (SC) {
+      if (tid < WAVE) {
+        const uint32_t nin = wave_reduce(sh.hist[HIST_WORDS + tid], OpAdd{});
+        if (tid == 0) {
           const uint32_t P = elem_bits(NEG_INF_RAW);
-          const uint32_t w = sh.hist[P >> 1];
-          const uint32_t cur = (P & 1u) ? (w >> 16) : (w & 0xFFFFu);
-          add = min(nin, 0xFFFFu - cur);
-          sh.hist[P >> 1] = w + ((P & 1u) ? (add << 16) : add);
+          bool heavy = false;
+          for (uint32_t k = 0; k < sh.n_heavy; ++k) heavy |= sh.hv_order[k] == order16(P);
+          uint32_t add = 0;
+          if (nin != 0u && !heavy) {
+            const uint32_t w = sh.hist[P >> 1];
+            const uint32_t cur = (P & 1u) ? (w >> 16) : (w & 0xFFFFu);
+            add = min(nin, 0xFFFFu - cur);
+            sh.hist[P >> 1] = w + ((P & 1u) ? (add << 16) : add);
+          }
+          sh.inf_extra = heavy ? 0u : nin - add;
         }
-        sh.inf_extra = nin - add;
       }
+      __syncthreads();
+      inf_extra = sh.inf_extra;
+      inf_order = order16(elem_bits(NEG_INF_RAW));
     }
-    __syncthreads();
-    inf_extra = sh.inf_extra;
-    inf_order = order16(elem_bits(NEG_INF_RAW));
-  }
+  };
+  // (the recounting body: every count, exact, the penalty's moves included)
+  if constexpr (HEAVY) heavy_recount<D>(sh, row, V, nfull, ALIGNED != 0, SC_ELEM, CAP, hid, H, pen, RP);
+  merge_neg_inf();
+
   FL_MARK(2);
 
+  const bool fast = fast_row;
   // ------------------------------------------------ compact to entries
   // Order o = 0 is the largest value.  Step s covers orders 128s .. 128s+127
   // (64 histogram words); wave w takes steps w, w + 16, ..., w + 496, so the
@@ -520,9 +678,13 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
   uint32_t* ent = sh.hist;
   // an entry's count: its 16 bits, and for the -cap entry of a soft-capped
   // row the -inf values beyond them
+  const uint32_t n_heavy = sh.n_heavy;
   auto entry_count = [&](uint32_t en) -> uint32_t {
-    if constexpr (SC) return (en & 0xFFFFu) + ((en >> 16) == inf_order ? inf_extra : 0u);
-    else return en & 0xFFFFu;
+    uint32_t c = en & 0xFFFFu;
+    if constexpr (SC) c += (en >> 16) == inf_order ? inf_extra : 0u;
+    if constexpr (HEAVY)  // counts beyond 16 bits of the patterns with more than 65535 values
+      for (uint32_t k = 0; k < n_heavy; ++k) c += (en >> 16) == sh.hv_order[k] ? sh.hv_extra[k] : 0u;
+    return c;
   };
   const bool cached = N <= CACHE_MAX;
   float* Yc = reinterpret_cast<float*>(sh.hist + N);
@@ -586,6 +748,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     }
     // a total other than V less the -inf values means a 16-bit counter
     // wrapped (> 65535 equal values)
+    // (more than 65535 equal values: FL_ROW_LIMIT, sampled by the exact-count kernel)
     if (tid == 0 && tc != static_cast<uint32_t>(V) && tc + neg_inf_count() != static_cast<uint32_t>(V))
       atomicOr(&sh.status, FL_ROW_LIMIT);
   }
@@ -826,7 +989,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       if constexpr (SC) r[j] = fast ? buf_load16(rrow, 16u * tid, 16u * NT * j) : make_uint4(0, 0, 0, 0);
-      else r[j] = d[j];
+      else if constexpr (!HEAVY) r[j] = d[j];
+      else r[j] = make_uint4(0, 0, 0, 0);
     }
     // the logits of this thread's first HPRE history ids again (keeping them
     // in VGPRs since the count pass would spill them), issued now so that the
@@ -857,8 +1021,23 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
     // slot of rank r do the threads form their members, and a block scan
     // picks the one of rank r.
     uint32_t* hlist[2] = {sh.hist, sh.hist + HLIST_CAP};
+    // The history bitmap: sh.hbits, or for a row past TILE_V (whose
+    // de-duplication used two windows of it) every id's bit, set here in the
+    // histogram's memory past the two member lists.
+    uint32_t* hb = sh.hbits;
+    if (pen && wide) {
+      hb = sh.hist + 2 * HLIST_CAP;
+      static_assert(2 * HLIST_CAP + FL_MAX_VOCAB_16 / 32 <= HIST_WORDS, "the full history bitmap fits");
+      for (int i = tid; i < FL_MAX_VOCAB_16 / 32; i += NT) hb[i] = 0u;
+      __syncthreads();
+      for (int i = tid; i < H; i += NT) {
+        const int id = hid[i];
+        if (id >= 0 && id < V) atomicOr(&hb[id >> 5], 1u << (id & 31));
+      }
+      __syncthreads();
+    }
     auto in_range = [&](int t, uint32_t bits) { return order16(bits) - o_lo[t] <= o_hi[t] - o_lo[t]; };
-    auto is_hist = [&](int idx) { return pen && ((sh.hbits[idx >> 5] >> (idx & 31)) & 1u); };
+    auto is_hist = [&](int idx) { return pen && ((hb[idx >> 5] >> (idx & 31)) & 1u); };
     auto push = [&](int t, int idx) {
       const uint32_t s = atomicAdd(&sh.nh[t], 1u);
       if (s < static_cast<uint32_t>(HLIST_CAP)) hlist[t][s] = idx;
@@ -871,7 +1050,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       for (int e = 0; e < 8; ++e) m |= in_range(t, elem_bits((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu)) ? (1u << e) : 0u;
       const int nv = V - c * 8;
       uint32_t valid = nv >= 8 ? 0xFFu : (nv > 0 ? (1u << nv) - 1u : 0u);
-      if (pen) valid &= ~(sh.hbits[c >> 2] >> ((c & 3) * 8));
+      if (pen) valid &= ~(hb[c >> 2] >> ((c & 3) * 8));
       return m & valid;
     };
     const int nchunks = (V + 7) >> 3;
@@ -993,7 +1172,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
 #pragma unroll
       for (int k = 0; k < HPRE; ++k)
         if (own[k]) hist_candidate(hpre[k], xh2[k]);
-      for (int i = tid + (hist_rows ? HPRE * NT : 0); i < H; i += NT) {
+      // (wide rows claimed every id in the windowed pass: none was prefetched)
+      for (int i = tid + ((hist_rows && !wide && !HEAVY) ? HPRE * NT : 0); i < H; i += NT) {
         if (!((sh.owner[i >> 5] >> (i & 31)) & 1u)) continue;
         const int id = hid[i];
         hist_candidate(id, row[id]);
@@ -1147,6 +1327,25 @@ __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, co
       a.out_desc[b] = dsc;
     }
   }
+  return true;
+}
+
+// The row sampler.  A row with more than 65535 equal values (a wrapped
+// 16-bit counter, seen by the entry pass) reports FL_ROW_LIMIT; the
+// exact-count kernel (FL_FLAG_EXACT_COUNTS) samples it.  (The exact body in
+// this kernel, even never run, costs every row ~6 us: the register
+// allocation of the common path gets worse.)
+template <class D, bool SC>
+__global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN) {
+  __shared__ Shared16 sh;
+  row_body<D, SC, false>(a, ALIGNED, SC_ELEM_IN, sh);
+}
+
+template <class D, bool SC>
+__global__ __launch_bounds__(NT) void k_sample_rows16_exact(const fl_sample_args a, const int ALIGNED,
+                                                            const int SC_ELEM_IN) {
+  __shared__ Shared16 sh;
+  row_body<D, SC, true>(a, ALIGNED, SC_ELEM_IN, sh);
 }
 
 // ------------------------------------------------------------------ launch
@@ -1156,12 +1355,23 @@ hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s) {
   const int sc_elem = (a.softcap > 0.0f && has_pen) ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(a.batch)), block(NT);
   const bool sc = a.softcap > 0.0f;
+  const bool exact = (a.flags & FL_FLAG_EXACT_COUNTS) != 0;
   if (a.dtype == FL_DTYPE_BF16) {
-    if (sc) hipLaunchKernelGGL((k_sample_rows16<BF16, true>), grid, block, 0, s, a, aligned, sc_elem);
-    else hipLaunchKernelGGL((k_sample_rows16<BF16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    if (exact) {
+      if (sc) hipLaunchKernelGGL((k_sample_rows16_exact<BF16, true>), grid, block, 0, s, a, aligned, sc_elem);
+      else hipLaunchKernelGGL((k_sample_rows16_exact<BF16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    } else {
+      if (sc) hipLaunchKernelGGL((k_sample_rows16<BF16, true>), grid, block, 0, s, a, aligned, sc_elem);
+      else hipLaunchKernelGGL((k_sample_rows16<BF16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    }
   } else {
-    if (sc) hipLaunchKernelGGL((k_sample_rows16<F16, true>), grid, block, 0, s, a, aligned, sc_elem);
-    else hipLaunchKernelGGL((k_sample_rows16<F16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    if (exact) {
+      if (sc) hipLaunchKernelGGL((k_sample_rows16_exact<F16, true>), grid, block, 0, s, a, aligned, sc_elem);
+      else hipLaunchKernelGGL((k_sample_rows16_exact<F16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    } else {
+      if (sc) hipLaunchKernelGGL((k_sample_rows16<F16, true>), grid, block, 0, s, a, aligned, sc_elem);
+      else hipLaunchKernelGGL((k_sample_rows16<F16, false>), grid, block, 0, s, a, aligned, sc_elem);
+    }
   }
   return hipGetLastError();
 }

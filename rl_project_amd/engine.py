@@ -141,6 +141,10 @@ class BatchedSampler:
         call.args.uniforms = uniforms.data_ptr()
         call.keep = (logits, uniforms)   # alive until the kernel has read them
         call.run()
+        # 16-bit rows where one value fills more than 65535 positions: the
+        # exact-count repeat (a kernel that leaves every other row alone)
+        if logits.size(1) > 0xFFFF:
+            call.run_exact_for_limited()
         return SampleOutput(call.tokens, call.finished[:n].view(torch.bool), call.status, call.logprob)
 
     def _step_slots(self, logits, uniforms, return_logprobs, slots) -> SampleOutput:
@@ -155,6 +159,8 @@ class BatchedSampler:
                      min_p=self.min_p[idx], repetition_penalty=self.rep_penalty[idx], history=(hist, hlen),
                      stop_ids=self.stop_ids[idx], uniforms=uniforms, finished=fin, out_finished=fin,
                      flags=_lib.FL_FLAG_APPEND_HISTORY, want_logprob=return_logprobs).run()
+        if logits.size(1) > 0xFFFF:
+            call.run_exact_for_limited()
         self.history.index_copy_(0, idx, hist)
         self.hist_len.index_copy_(0, idx, hlen)
         self.finished_u8.index_copy_(0, idx, fin)

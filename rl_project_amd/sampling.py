@@ -191,6 +191,29 @@ class _Call:
         check(lib().fl_sample(ctypes.byref(self.args), self.stream), "fl_sample")
         return self
 
+    def run_exact_for_limited(self) -> "_Call":
+        """Repeat the call for the rows it left at FL_ROW_LIMIT with the
+        exact-count kernel (16-bit rows where one value fills more than 65535
+        positions); every other row keeps its outputs.  Stream-ordered, no
+        host synchronisation (the kernel reads the status)."""
+        if self.logits.dtype == torch.float32:
+            return self
+        flags = self.args.flags
+        self.args.flags = flags | _lib.FL_FLAG_EXACT_COUNTS | _lib.FL_FLAG_ONLY_LIMITED
+        try:
+            check(lib().fl_sample(ctypes.byref(self.args), self.stream), "fl_sample")
+        finally:
+            self.args.flags = flags
+        return self
+
+    def run_checked(self) -> "_Call":
+        """run(), then the exact-count repeat if a 16-bit row reports
+        FL_ROW_LIMIT (synchronises with the host to read the status)."""
+        self.run()
+        if self.logits.dtype != torch.float32 and bool(((self.status & _lib.FL_ROW_LIMIT) != 0).any()):
+            self.run_exact_for_limited()
+        return self
+
 
 class SamplerPlan:
     """A prepared ``sample_tokens`` call: arguments and output buffers are
@@ -199,18 +222,23 @@ class SamplerPlan:
     Reads ``logits`` and the parameter tensors at launch time, so callers may
     overwrite them in place between launches."""
 
-    def __init__(self, logits: torch.Tensor, **kw):
+    def __init__(self, logits: torch.Tensor, exact_repeat: bool = False, **kw):
         want_logprob = kw.pop("return_logprobs", False)
         want_desc = kw.pop("return_desc", False)
         self._call = _Call(logits, flags=0, want_logprob=want_logprob, want_desc=want_desc,
                            finished=kw.pop("finished", None), uniforms=kw.pop("uniforms", None), **kw)
         self._fn = lib().fl_sample
         self._argp = ctypes.byref(self._call.args)
+        # exact_repeat: every launch also enqueues the exact-count repeat for
+        # rows left at FL_ROW_LIMIT (one more kernel; no host synchronisation)
+        self._exact = exact_repeat and logits.dtype != torch.float32
 
     def launch(self) -> None:
         rc = self._fn(self._argp, self._call.stream)
         if rc:
             check(rc, "fl_sample")
+        if self._exact:
+            self._call.run_exact_for_limited()
 
     @property
     def output(self) -> SampleOutput:
@@ -263,16 +291,19 @@ def sample_tokens(
     call = _Call(logits, temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
                  repetition_penalty=repetition_penalty, history=history, stop_ids=stop_ids, uniforms=uniforms,
                  finished=finished, softcap=softcap, flags=0, want_logprob=return_logprobs,
-                 want_desc=return_desc).run()
+                 want_desc=return_desc)
     if check_status:
+        call.run_checked()
         _raise_on_status(call.status)
+    else:
+        call.run()
     return SampleOutput(call.tokens, call.finished.bool(), call.status, call.logprob, call.desc)
 
 
 def describe_rows(logits: torch.Tensor, **kw) -> Tuple[torch.Tensor, torch.Tensor]:
     """Descriptors of the filtered distribution of every row (no selection)."""
     call = _Call(logits, flags=FL_FLAG_NO_SELECT, want_logprob=False, want_desc=True, uniforms=None,
-                 finished=None, **kw).run()
+                 finished=None, **kw).run_checked()
     return call.desc, call.status
 
 
@@ -280,7 +311,7 @@ def filtered_outputs(logits: torch.Tensor, *, want_filtered: bool = True, want_p
                      want_mask: bool = False, **kw):
     """(filtered logits, probabilities, keep bit-mask, status) of every row; any may be skipped."""
     call = _Call(logits, flags=FL_FLAG_NO_SELECT, want_logprob=False, want_desc=True, uniforms=None,
-                 finished=None, **kw).run()
+                 finished=None, **kw).run_checked()
     B, V = call.B, call.V
     dev = call.logits.device
     out = torch.empty(B, V, dtype=call.logits.dtype, device=dev) if want_filtered else None

@@ -106,7 +106,10 @@ def _args(**kw):
     (dict(out_token=None), _lib.FL_EINVAL, "out_token"),
     (dict(hist_ids=0x3000), _lib.FL_EINVAL, "hist_len"),
     (dict(n_stop=2), _lib.FL_EINVAL, "stop"),
-    (dict(flags=4), _lib.FL_EINVAL, "flags"),
+    (dict(flags=16), _lib.FL_EINVAL, "flags"),
+    (dict(flags=_lib.FL_FLAG_ONLY_LIMITED), _lib.FL_EINVAL, "ONLY_LIMITED"),
+    (dict(flags=_lib.FL_FLAG_ONLY_LIMITED | _lib.FL_FLAG_EXACT_COUNTS, out_status=None), _lib.FL_EINVAL,
+     "ONLY_LIMITED"),
     (dict(uniform_div=-1), _lib.FL_EINVAL, "uniform_div"),
     (dict(flags=_lib.FL_FLAG_APPEND_HISTORY), _lib.FL_EINVAL, "APPEND_HISTORY"),
     (dict(flags=_lib.FL_FLAG_APPEND_HISTORY, hist_ids=0x3000, hist_len=0x3100, hist_ld=0), _lib.FL_EINVAL,

@@ -41,8 +41,7 @@ def random_case(seed: int) -> workloads.SampleWorkload:
     K = torch.tensor([rng.choice([0, 1, 5, 50, 1000]) for _ in range(B)], dtype=torch.int32)
     P = torch.tensor([rng.choice([1.0, 0.5, 0.9, 0.99]) for _ in range(B)])
     MP = torch.tensor([rng.choice([0.0, 0.0, 0.05, 0.3]) for _ in range(B)])
-    pen_ok = not (dt != torch.float32 and V > 131072)   # the 16-bit history bitmap covers 131072 values
-    RP = torch.tensor([rng.choice([1.0, 1.2, 0.8]) if pen_ok else 1.0 for _ in range(B)])
+    RP = torch.tensor([rng.choice([1.0, 1.2, 0.8]) for _ in range(B)])
     H = rng.choice([0, 8, 300])
     hist = torch.randint(0, V, (B, H), generator=g, dtype=torch.int32) if H else None
     if hist is not None and rng.random() < 0.5:
