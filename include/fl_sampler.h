@@ -227,6 +227,19 @@ int fl_spec_verify(const fl_spec_args* args, void* stream);
 int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes);
 
 /*
+ * fl_spec_verify on its sliced path with no workspace argument and no
+ * allocation: the scratch is a static device array of the library, one copy
+ * per GPU, held until the process ends, for up to FL_SPEC_STATIC_MAX_BATCH
+ * sequences (FL_ENOTSUP beyond).  args->workspace must be NULL and
+ * workspace_bytes 0.  No counterpart in the reference: for callers that
+ * cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  Results equal fl_spec_verify's.  Every call on a GPU shares its
+ * array: calls that overlap in time on one GPU race.
+ */
+#define FL_SPEC_STATIC_MAX_BATCH 4096
+int fl_spec_verify_static(const fl_spec_args* args, void* stream);
+
+/*
  * Full-distribution statistics of `rows` logits rows in one pass, in float32
  * as the reference computes them after .float():
  *   out_logprob[r] = -cross_entropy(x_r, labels[r])   (models/policy.py:47-50;

@@ -26,6 +26,7 @@ FL_FLAG_EXACT_COUNTS = 4
 FL_FLAG_ONLY_LIMITED = 8
 FL_MAX_VOCAB_F32 = 262144
 FL_MAX_VOCAB_16 = 262144
+FL_SPEC_STATIC_MAX_BATCH = 4096
 FL_MAX_HISTORY = 65536
 
 ROW_STATUS_NAMES = {
@@ -107,6 +108,8 @@ def lib() -> ctypes.CDLL:
     handle.fl_apply_filter.restype = ctypes.c_int
     handle.fl_spec_verify.argtypes = [ctypes.POINTER(SpecArgs), _p]
     handle.fl_spec_verify.restype = ctypes.c_int
+    handle.fl_spec_verify_static.argtypes = [ctypes.POINTER(SpecArgs), _p]
+    handle.fl_spec_verify_static.restype = ctypes.c_int
     handle.fl_spec_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
     handle.fl_spec_workspace_bytes.restype = ctypes.c_int
     handle.fl_row_stats.argtypes = [ctypes.POINTER(RowStatsArgs), _p]
@@ -132,5 +135,6 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_workspace_bytes", "fl_row_stats",
+EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_verify_static",
+                    "fl_spec_workspace_bytes", "fl_row_stats",
                     "fl_last_error", "fl_abi_version")

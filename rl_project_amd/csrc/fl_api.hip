@@ -105,22 +105,29 @@ int fl_apply_filter(const fl_sample_args* a, const fl_row_desc* desc, void* out_
   return check_launch(e, "fl_apply_filter");
 }
 
-int fl_spec_verify(const fl_spec_args* a, void* stream) {
-  if (a == nullptr) return fail(FL_EINVAL, "fl_spec_verify: args is NULL");
-  if (a->struct_size != sizeof(fl_spec_args)) return fail(FL_EINVAL, "fl_spec_verify: struct_size mismatch");
+// The checks shared by fl_spec_verify and fl_spec_verify_static; 1 = go on.
+int validate_spec(const fl_spec_args* a, const char* fn) {
+  if (a == nullptr) return fail(FL_EINVAL, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(fl_spec_args)) return fail(FL_EINVAL, "%s: struct_size mismatch", fn);
   if (a->dtype != FL_DTYPE_F32 && a->dtype != FL_DTYPE_BF16 && a->dtype != FL_DTYPE_F16)
-    return fail(FL_EINVAL, "fl_spec_verify: unknown dtype %d", a->dtype);
+    return fail(FL_EINVAL, "%s: unknown dtype %d", fn, a->dtype);
   if (a->batch < 0 || a->k < 1 || a->vocab < 1 || a->ld < a->vocab)
-    return fail(FL_EINVAL, "fl_spec_verify: bad shape batch=%lld k=%lld vocab=%lld ld=%lld",
+    return fail(FL_EINVAL, "%s: bad shape batch=%lld k=%lld vocab=%lld ld=%lld", fn,
                 static_cast<long long>(a->batch), static_cast<long long>(a->k), static_cast<long long>(a->vocab),
                 static_cast<long long>(a->ld));
   if (a->vocab > FL_MAX_VOCAB_F32 || a->batch > 0x7fffffff)
-    return fail(FL_ENOTSUP, "fl_spec_verify: vocab %lld or batch %lld beyond the library's limits",
+    return fail(FL_ENOTSUP, "%s: vocab %lld or batch %lld beyond the library's limits", fn,
                 static_cast<long long>(a->vocab), static_cast<long long>(a->batch));
   if (a->batch == 0) return ok();
   if (!a->temperature || !a->target || !a->draft || !a->target_desc || !a->draft_desc || !a->draft_ids || !a->u_accept ||
       !a->u_resample || !a->bonus_token || !a->out_n_accepted || !a->out_tokens)
-    return fail(FL_EINVAL, "fl_spec_verify: a required pointer is NULL");
+    return fail(FL_EINVAL, "%s: a required pointer is NULL", fn);
+  return 1;
+}
+
+int fl_spec_verify(const fl_spec_args* a, void* stream) {
+  const int v = validate_spec(a, "fl_spec_verify");
+  if (v != 1) return v;
   if (a->workspace != nullptr && (a->workspace_bytes < 0 ||
                                   static_cast<size_t>(a->workspace_bytes) < fl::spec_workspace_bytes(a->batch)))
     return fail(FL_EINVAL, "fl_spec_verify: workspace of %lld bytes, %zu needed", static_cast<long long>(a->workspace_bytes),
@@ -129,6 +136,19 @@ int fl_spec_verify(const fl_spec_args* a, void* stream) {
     return fail(FL_EINVAL, "fl_spec_verify: workspace not 8-byte aligned");
   const hipError_t e = fl::launch_spec_verify(*a, static_cast<hipStream_t>(stream));
   return check_launch(e, "fl_spec_verify");
+}
+
+int fl_spec_verify_static(const fl_spec_args* a, void* stream) {
+  const int v = validate_spec(a, "fl_spec_verify_static");
+  if (v != 1) return v;
+  if (a->workspace != nullptr || a->workspace_bytes != 0)
+    return fail(FL_EINVAL, "fl_spec_verify_static: workspace must be NULL with workspace_bytes 0 (the library's "
+                "static scratch is used)");
+  if (a->batch > FL_SPEC_STATIC_MAX_BATCH || fl::spec_workspace_bytes(a->batch) > fl::spec_static_scratch_bytes())
+    return fail(FL_ENOTSUP, "fl_spec_verify_static: batch %lld exceeds the %d sequences of the static scratch",
+                static_cast<long long>(a->batch), FL_SPEC_STATIC_MAX_BATCH);
+  const hipError_t e = fl::launch_spec_verify_static(*a, static_cast<hipStream_t>(stream));
+  return check_launch(e, "fl_spec_verify_static");
 }
 
 int fl_row_stats(const fl_row_stats_args* a, void* stream) {

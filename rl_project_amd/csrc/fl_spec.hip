@@ -16,6 +16,8 @@
 //            place of torch.multinomial, :75), with masses in exact 2^-45
 //            fixed point and the order kept by thread-contiguous row slices
 //   bonus    every draft accepted: the target sample of position K (:79-84)
+#include <mutex>
+
 #include "fl_device.h"
 #include "fl_kernels.h"
 
@@ -466,9 +468,57 @@ __global__ __launch_bounds__(NT) void k_spec_pick(const fl_spec_args a, SpecWs w
 
 size_t spec_workspace_bytes(int64_t batch) { return spec_ws_bytes(batch); }
 
-hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s) {
-  const bool sliced = a.workspace != nullptr;
-  const SpecWs ws = sliced ? spec_ws(a.workspace, a.batch) : SpecWs{};
+// ---------------------------------------------------------------- scratch that needs no allocation
+// The sliced path's workspace for up to FL_SPEC_STATIC_MAX_BATCH sequences
+// (20 bytes a sequence at 4096 of them; at most 40 KiB below 2048), one copy on
+// each GPU the library runs on, held until the process ends.  Every byte a
+// call reads was written earlier in the same call (the accept kernel writes
+// each sequence's state, the slice kernels each part they later read), so
+// nothing is cleared between calls; calls that overlap on one GPU race.
+constexpr size_t SPEC_STATIC_BYTES = 81920;
+static __device__ __align__(256) unsigned char scratch[SPEC_STATIC_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};  // the device address of `scratch`, per device
+}  // namespace
+
+size_t spec_static_scratch_bytes() { return SPEC_STATIC_BYTES; }
+
+// The device address of this GPU's `scratch` (the name itself is a host-side
+// stand-in, never a device address), looked up once per device with that
+// device current.
+hipError_t spec_static_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s) { return launch_spec_verify_on(a, a.workspace, s); }
+
+hipError_t launch_spec_verify_static(const fl_spec_args& a, hipStream_t s) {
+  if (spec_ws_bytes(a.batch) > SPEC_STATIC_BYTES) return hipErrorInvalidValue;  // (the caller checks first)
+  void* p = nullptr;
+  const hipError_t e = spec_static_scratch(&p);
+  if (e != hipSuccess) return e;
+  return launch_spec_verify_on(a, p, s);
+}
+
+hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, hipStream_t s) {
+  const bool sliced = workspace != nullptr;
+  const SpecWs ws = sliced ? spec_ws(workspace, a.batch) : SpecWs{};
   const dim3 grid(static_cast<unsigned>(a.batch));
   auto run = [&](auto tag) {
     using D = decltype(tag);

@@ -44,13 +44,16 @@ class SpecPlan:
     loop may overwrite them in place between launches.  ``sliced`` spreads the
     residual draw of each rejected sequence over several work-groups (with a
     workspace allocated here); ``sliced=False`` runs one work-group per
-    sequence.  Both give identical results."""
+    sequence; ``no_alloc=True`` runs the sliced path on the library's static
+    device scratch (``fl_spec_verify_static``: no workspace, at most 4096
+    sequences, plans that launch at the same time on one GPU race).  All give
+    identical results."""
 
     def __init__(self, target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_ids: torch.Tensor, *,
                  temperature: float = 1.0, top_k: Optional[int] = None, top_p: Optional[float] = None,
                  min_p: Optional[float] = None, softcap: float = 0.0, u_accept: Optional[torch.Tensor] = None,
                  u_resample: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
-                 return_ratio: bool = True, sliced: bool = True):
+                 return_ratio: bool = True, sliced: bool = True, no_alloc: bool = False):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
             raise ValueError("target_logits must be [B, K+1, V] and draft_logits [B, K, V]")
         B, K1, V = target_logits.shape
@@ -95,6 +98,9 @@ class SpecPlan:
         a.out_n_accepted, a.out_tokens, a.out_ratio = (self.n_accepted.data_ptr(), self.tokens.data_ptr(),
                                                        ptr(self.ratio))
         # scratch of the sliced residual draw (several work-groups per sequence)
+        if no_alloc and B > _lib.FL_SPEC_STATIC_MAX_BATCH:
+            raise ValueError(f"no_alloc verifies at most {_lib.FL_SPEC_STATIC_MAX_BATCH} sequences, not {B}")
+        sliced = sliced and not no_alloc
         nbytes = ctypes.c_size_t(0)
         check(lib().fl_spec_workspace_bytes(B, ctypes.byref(nbytes)), "fl_spec_workspace_bytes")
         self._ws = torch.empty(max(int(nbytes.value), 8), dtype=torch.uint8, device=dev) if sliced else None
@@ -103,14 +109,14 @@ class SpecPlan:
         self._args = a
         self._argp = ctypes.byref(a)
         self._stream = _lib.stream_handle(dev)
-        self._verify = lib().fl_spec_verify
+        self._verify = lib().fl_spec_verify_static if no_alloc else lib().fl_spec_verify
 
     def launch(self) -> None:
         self._t.run()
         self._d.run()
         rc = self._verify(self._argp, self._stream)
         if rc:
-            check(rc, "fl_spec_verify")
+            check(rc, self._verify.__name__)
 
     def status_ok(self) -> torch.Tensor:
         """bool [B]: every target and draft row of the sequence could be sampled."""

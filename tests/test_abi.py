@@ -156,6 +156,38 @@ def test_spec_argument_errors():
     assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL
 
 
+def test_spec_verify_static_argument_errors():
+    """The allocation-free verify: the shared checks, a workspace refused,
+    the batch bounded by the static scratch (4096 sequences, whose sliced
+    workspace fits its 80 KiB), all before anything touches a GPU."""
+    L = _lib.lib()
+    s = _lib.SpecArgs()
+    s.struct_size = ctypes.sizeof(_lib.SpecArgs)
+    s.dtype, s.batch, s.k, s.vocab, s.ld = _lib.FL_DTYPE_F32, 2, 0, 10, 10
+    assert L.fl_spec_verify_static(ctypes.byref(s), None) == _lib.FL_EINVAL       # k < 1
+    assert "fl_spec_verify_static" in L.fl_last_error().decode()
+    s.k = 3
+    assert L.fl_spec_verify_static(ctypes.byref(s), None) == _lib.FL_EINVAL       # NULL pointers
+    for f in ("temperature", "target", "draft", "target_desc", "draft_desc", "draft_ids", "u_accept", "u_resample",
+              "bonus_token", "out_n_accepted", "out_tokens"):
+        setattr(s, f, 0x10000)
+    s.workspace, s.workspace_bytes = 0x20000, 1 << 20
+    assert L.fl_spec_verify_static(ctypes.byref(s), None) == _lib.FL_EINVAL
+    assert "workspace must be NULL" in L.fl_last_error().decode()
+    s.workspace, s.workspace_bytes = None, 0
+    s.batch = _lib.FL_SPEC_STATIC_MAX_BATCH + 1
+    assert L.fl_spec_verify_static(ctypes.byref(s), None) == _lib.FL_ENOTSUP
+    assert "static scratch" in L.fl_last_error().decode()
+    n = ctypes.c_size_t(0)
+    worst = 0
+    for b in range(1, _lib.FL_SPEC_STATIC_MAX_BATCH + 1):
+        assert L.fl_spec_workspace_bytes(b, ctypes.byref(n)) == _lib.FL_OK
+        worst = max(worst, n.value)
+    assert worst == 20 * 4096 == 81920
+    s.batch = 0
+    assert L.fl_spec_verify_static(ctypes.byref(s), None) == _lib.FL_OK
+
+
 def test_spec_workspace_bytes_and_checks():
     L = _lib.lib()
     n = ctypes.c_size_t(0)

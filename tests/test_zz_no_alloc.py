@@ -1,0 +1,73 @@
+"""The allocation-free verify entry point, fl_spec_verify_static (MI355X).
+
+It runs fl_spec_verify's sliced path on the library's static device scratch
+instead of a caller's workspace.  Each case prepares a SpecPlan with a
+workspace (fl_spec_verify), launches it, then calls fl_spec_verify_static
+through the C ABI on the same arguments with the workspace taken away and
+fresh outputs; accepted counts, tokens and acceptance ratios must be equal
+bit for bit.  The calls come one after another with shrinking batches, so
+the scratch holds a larger call's contents when a smaller one starts."""
+
+import ctypes
+
+import pytest
+import torch
+
+from rl_project_amd import _lib
+from rl_project_amd.speculative import SpecPlan
+
+pytestmark = pytest.mark.gpu
+
+# (sequences, drafts, vocabulary, dtype): the largest batch the scratch holds,
+# the speculative benchmark's shape, then a small bf16 one
+CASES = [(4096, 2, 1000, torch.float32), (32, 5, 128256, torch.float32), (7, 3, 32000, torch.bfloat16)]
+
+
+def _plan(B, K, V, dtype, seed, no_alloc=False):
+    g = torch.Generator().manual_seed(seed)
+    target = (torch.randn(B, K + 1, V, generator=g) * 2.0).to(dtype)
+    draft = (target[:, :K].float() + torch.randn(B, K, V, generator=g) * 1.5).to(dtype)
+    # drafts: half the target's argmax (often accepted), half random (often rejected)
+    ids = torch.randint(0, V, (B, K), generator=g)
+    am = target[:, :K].float().argmax(-1)
+    ids = torch.where(torch.rand(B, K, generator=g) < 0.5, am, ids)
+    u_acc = torch.rand(B, K, generator=g)
+    u_res = torch.rand(B, generator=g)
+    return SpecPlan(target.cuda(), draft.cuda(), ids.cuda(), temperature=0.9, top_p=0.95,
+                    u_accept=u_acc.cuda(), u_resample=u_res.cuda(), sliced=True, no_alloc=no_alloc)
+
+
+def _static_call(plan):
+    """fl_spec_verify_static on the plan's arguments, no workspace, fresh outputs."""
+    a = _lib.SpecArgs()
+    ctypes.memmove(ctypes.byref(a), ctypes.byref(plan._args), ctypes.sizeof(a))
+    a.workspace, a.workspace_bytes = None, 0
+    n = torch.full_like(plan.n_accepted, -7)
+    t = torch.full_like(plan.tokens, -7)
+    r = torch.full_like(plan.ratio, -7.0)
+    a.out_n_accepted, a.out_tokens, a.out_ratio = n.data_ptr(), t.data_ptr(), r.data_ptr()
+    rc = _lib.lib().fl_spec_verify_static(ctypes.byref(a), plan._stream)
+    assert rc == _lib.FL_OK, _lib.lib().fl_last_error().decode()
+    return n, t, r
+
+
+def test_static_scratch_verify_matches_the_workspace_verify():
+    for i, (B, K, V, dtype) in enumerate(CASES):
+        print(f"[no-alloc verify] call {i}: B={B} K={K} V={V} {dtype}", flush=True)
+        plan = _plan(B, K, V, dtype, seed=100 + i)
+        plan.launch()
+        n, t, r = _static_call(plan)
+        torch.cuda.synchronize()
+        assert bool(plan.status_ok().all())
+        rejected = int((plan.n_accepted < K).sum())
+        print(f"   {rejected} of {B} sequences resampled", flush=True)
+        assert rejected > 0     # the residual draw, which uses the scratch, ran
+        assert torch.equal(n, plan.n_accepted)
+        assert torch.equal(t, plan.tokens)
+        assert torch.equal(r.view(torch.int32), plan.ratio.view(torch.int32))
+        # and the plan's own no_alloc form, the same outputs again
+        p2 = _plan(B, K, V, dtype, seed=100 + i, no_alloc=True)
+        assert p2._ws is None and p2._args.workspace is None
+        p2.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(p2.n_accepted, plan.n_accepted) and torch.equal(p2.tokens, plan.tokens)
