@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
 import torch
 
@@ -149,11 +149,53 @@ def speculative_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, 
     return plan.output
 
 
+def _as_sequences(idx) -> tuple:
+    """(list of 1-D token tensors, whether the caller passed one [1, T] tensor)."""
+    if isinstance(idx, torch.Tensor):
+        if idx.dim() != 2:
+            raise ValueError("idx must be [B, T] or a list of 1-D token tensors")
+        return [idx[b] for b in range(idx.size(0))], idx.size(0) == 1
+    seqs = [t.reshape(-1) for t in idx]
+    if not seqs:
+        raise ValueError("no sequences")
+    return seqs, False
+
+
+def _grouped(fn, ctxs: List[torch.Tensor]) -> List:
+    """fn over the contexts, one call per group of equal length (a model
+    forward takes [g, L] token ids); the results of row i of each call, in
+    the order of ``ctxs``."""
+    groups: Dict[int, List[int]] = {}
+    for i, c in enumerate(ctxs):
+        groups.setdefault(int(c.numel()), []).append(i)
+    out: List = [None] * len(ctxs)
+    for members in groups.values():
+        res = fn(torch.stack([ctxs[i] for i in members]))
+        for j, i in enumerate(members):
+            out[i] = tuple(r[j] for r in res) if isinstance(res, tuple) else res[j]
+    return out
+
+
+def _result(seqs: List[torch.Tensor], single: bool):
+    return seqs[0].view(1, -1) if single else [s.view(1, -1) for s in seqs]
+
+
 class SpeculativeGenerator:
     """Draft ``k`` tokens with a small model, verify with the target in one
-    pass (reference ``speculative.py:20-91``, batched over sequences).
+    pass (reference ``speculative.py:20-91``), for a batch of sequences.
 
-    Models follow the reference protocol: ``model(idx) -> (logits [B, T, V], _)``,
+    Each sequence follows the reference's one-sequence loop; the sequences of
+    a batch advance together: per round, the draft model runs once per group
+    of equal context length, each of the ``k`` draft draws is one sampler
+    launch over every active sequence, the target runs once per length group,
+    and one batched verify decides all of them (ragged acceptance: each
+    sequence keeps its own accepted drafts plus its resampled or bonus token).
+
+    ``idx``: a [1, T] tensor (returns [1, T'], as the reference), a [B, T]
+    tensor or a list of 1-D prompts (returns a list of [1, T_b] tensors).
+    ``trace``: a list that receives, per round, the active sequences and every
+    draw and decision (for replay checks).  Models follow the reference
+    protocol: ``model(idx) -> (logits [B, T, V], _)``,
     ``model.full_logits(idx) -> [B, T, V]`` and ``model.spec.block_size``."""
 
     def __init__(self, target_model, draft_model, k: int = 5):
@@ -163,48 +205,75 @@ class SpeculativeGenerator:
         self.stats: Dict[str, int] = {"proposed": 0, "accepted": 0}
 
     @torch.no_grad()
-    def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 1.0, top_k: Optional[int] = 50,
-                 top_p: Optional[float] = None, generator: Optional[torch.Generator] = None) -> torch.Tensor:
-        if idx.size(0) != 1:
-            raise ValueError("SpeculativeGenerator.generate grows one sequence (use speculative_verify for batches)")
+    def generate(self, idx, max_new_tokens: int, temperature: float = 1.0, top_k: Optional[int] = 50,
+                 top_p: Optional[float] = None, generator: Optional[torch.Generator] = None,
+                 trace: Optional[List[dict]] = None):
+        seqs, single = _as_sequences(idx)
+        dev = seqs[0].device
         T = max(temperature, 1e-8)
-        generated = 0
-        while generated < max_new_tokens:
-            draft_tokens, draft_rows = [], []
-            draft_idx = idx.clone()
-            bs = self.draft.spec.block_size
-            for _ in range(self.k):
-                ctx = draft_idx if draft_idx.size(1) <= bs else draft_idx[:, -bs:]
-                logits, _ = self.draft(ctx)
-                row = logits[:, -1, :]
-                tok = sample_tokens(row, temperature=T, top_k=top_k or 0, top_p=top_p or 1.0,
-                                    uniforms=torch.rand(1, device=idx.device, generator=generator)).tokens.view(1, 1)
-                draft_tokens.append(tok)
-                draft_rows.append(row)
-                draft_idx = torch.cat([draft_idx, tok], dim=1)
-            verify_idx = torch.cat([idx] + draft_tokens, dim=1)
-            tb = self.target.spec.block_size
-            if verify_idx.size(1) > tb:
-                verify_idx = verify_idx[:, -tb:]
-            target_logits = self.target.full_logits(verify_idx)
-            prompt_len = idx.size(1)
-            offset = verify_idx.size(1) - (prompt_len + self.k)
-            first = prompt_len - 1 + offset
-            if first < 0 or first + self.k >= target_logits.size(1):
+        K = self.k
+        n = len(seqs)
+        generated = [0] * n
+        active = [max_new_tokens > 0] * n
+        bs, tb = self.draft.spec.block_size, self.target.spec.block_size
+        while True:
+            act = [b for b in range(n) if active[b]]
+            if not act:
                 break
-            out = speculative_verify(target_logits[:, first:first + self.k + 1, :].contiguous(),
-                                     torch.stack(draft_rows, dim=1), torch.cat(draft_tokens, dim=1),
-                                     temperature=T, top_k=top_k, top_p=top_p, generator=generator)
-            n = int(out.n_accepted[0])
-            self.stats["proposed"] += min(n + 1, self.k)
-            self.stats["accepted"] += n
-            new = out.tokens[0, : n + 1]
-            new = new[: max_new_tokens - generated]
-            idx = torch.cat([idx, new.view(1, -1)], dim=1)
-            generated += new.numel()
-            if idx.size(1) >= tb:
-                break
-        return idx
+            # k draft draws, each one launch over the active sequences
+            dctx = [seqs[b] for b in act]
+            d_rows, d_toks, u_draft = [], [], []
+            for _ in range(K):
+                rows = torch.stack(_grouped(lambda x: self.draft(x)[0][:, -1, :],
+                                            [c if c.numel() <= bs else c[-bs:] for c in dctx]))
+                u = torch.rand(len(act), device=dev, generator=generator)
+                tok = sample_tokens(rows, temperature=T, top_k=top_k or 0, top_p=top_p or 1.0, uniforms=u).tokens
+                d_rows.append(rows)
+                d_toks.append(tok)
+                u_draft.append(u)
+                dctx = [torch.cat([c, tok[i:i + 1].to(c.dtype)]) for i, c in enumerate(dctx)]
+            drafts = torch.stack(d_toks, dim=1)                     # [A, K]
+            vctx = [torch.cat([seqs[b], drafts[i].to(seqs[b].dtype)]) for i, b in enumerate(act)]
+            vctx = [c if c.numel() <= tb else c[-tb:] for c in vctx]
+            full = _grouped(lambda x: self.target.full_logits(x), vctx)
+            # the verify positions of each sequence: prompt_len - 1 + offset ..
+            # (+ K); the context is cut to the block size from the left
+            rows_t, ok = [], []
+            for i, b in enumerate(act):
+                L = vctx[i].numel()
+                first = seqs[b].numel() - 1 + (L - (seqs[b].numel() + K))
+                if first < 0 or first + K >= full[i].size(0):
+                    active[b] = False
+                    continue
+                rows_t.append(full[i][first:first + K + 1])
+                ok.append(i)
+            rec = {"seqs": act, "u_draft": torch.stack(u_draft, dim=1), "draft_tokens": drafts, "verified": ok}
+            if ok:
+                sel = torch.tensor(ok, device=dev)
+                u_acc = torch.rand(len(ok), K, device=dev, generator=generator)
+                u_res = torch.rand(len(ok), device=dev, generator=generator)
+                out = speculative_verify(torch.stack(rows_t), torch.stack(d_rows, dim=1)[sel].contiguous(),
+                                         drafts[sel].contiguous(), temperature=T, top_k=top_k, top_p=top_p,
+                                         u_accept=u_acc, u_resample=u_res, return_ratio=False)
+                n_acc = out.n_accepted.tolist()
+                toks = out.tokens.tolist()
+                rec.update(u_accept=u_acc, u_resample=u_res, n_accepted=n_acc, tokens=toks)
+                for j, i in enumerate(ok):
+                    b = act[i]
+                    room = max_new_tokens - generated[b]
+                    na = n_acc[j]
+                    # drafts examined as the reference's loop does: up to the
+                    # first rejection, or until the token budget is spent
+                    self.stats["proposed"] += room if room <= na else min(na + 1, K)
+                    self.stats["accepted"] += min(na, room)
+                    new = toks[j][: na + 1][:room]
+                    seqs[b] = torch.cat([seqs[b], torch.tensor(new, dtype=seqs[b].dtype, device=dev)])
+                    generated[b] += len(new)
+                    if generated[b] >= max_new_tokens or seqs[b].numel() >= tb:
+                        active[b] = False
+            if trace is not None:
+                trace.append(rec)
+        return _result(seqs, single)
 
     @property
     def acceptance_rate(self) -> float:
@@ -213,9 +282,9 @@ class SpeculativeGenerator:
 
 class MTPSpeculativeGenerator:
     """Self-speculative decoding with the model's multi-token-prediction heads
-    (reference ``speculative.py:94-158``), one sequence.
+    (reference ``speculative.py:94-158``), for a batch of sequences.
 
-    Per round, as the reference:
+    Per round and sequence, as the reference:
 
     1. ``token_1`` is sampled from the main head.
     2. Each MTP head drafts the next token from the last hidden state and the
@@ -225,9 +294,12 @@ class MTPSpeculativeGenerator:
        sequence: accept while ``u < min(1, p/q)``; the first rejection
        resamples ``max(0, p − q)``. A round draws no bonus token.
 
-    Filtering is the reference's ``_topk_filter(logits / T, top_k)``. Draws
-    are the build's inverse CDF with uniforms from ``generator``; the draws
-    and the verify run on the GPU path.  Model protocol: ``model(idx) ->
+    Batched: the main forward and the verify forward run once per group of
+    equal context length, the MTP heads and every draw once over all active
+    sequences, the verify in one launch (ragged acceptance).  Filtering is the
+    reference's ``_topk_filter(logits / T, top_k)``. Draws are the build's
+    inverse CDF with uniforms from ``generator``.  ``idx`` and ``trace`` as
+    for ``SpeculativeGenerator``.  Model protocol: ``model(idx) ->
     (logits, _)`` setting ``model._last_hidden``; ``model.full_logits``,
     ``model.mtp_modules``, ``model.transformer.wte``, ``model.lm_head``,
     ``model.spec.block_size``."""
@@ -239,66 +311,92 @@ class MTPSpeculativeGenerator:
         self.n_drafts = len(model.mtp_modules)
 
     @torch.no_grad()
-    def generate(self, idx: torch.Tensor, max_new_tokens: int = 200, temperature: float = 1.0,
-                 top_k: Optional[int] = 50, generator: Optional[torch.Generator] = None) -> torch.Tensor:
-        if idx.size(0) != 1:
-            raise ValueError("MTPSpeculativeGenerator.generate grows one sequence")
+    def generate(self, idx, max_new_tokens: int = 200, temperature: float = 1.0, top_k: Optional[int] = 50,
+                 generator: Optional[torch.Generator] = None, trace: Optional[List[dict]] = None):
+        seqs, single = _as_sequences(idx)
         self.model.eval()
         T = max(float(temperature), 1e-8)
         k = top_k if (top_k is not None and top_k > 0) else 0
-        dev = idx.device
+        dev = seqs[0].device
         block = self.model.spec.block_size
-        generated = 0
+        n = len(seqs)
+        generated = [0] * n
+        active = [max_new_tokens > 0] * n
 
-        def draw(row: torch.Tensor) -> torch.Tensor:
-            u = torch.rand(1, device=dev, generator=generator)
-            return sample_tokens(row, temperature=T, top_k=k, uniforms=u).tokens.view(1, 1)
+        def draw(rows: torch.Tensor, us: list) -> torch.Tensor:
+            u = torch.rand(rows.size(0), device=dev, generator=generator)
+            us.append(u)
+            return sample_tokens(rows, temperature=T, top_k=k, uniforms=u).tokens
 
-        while generated < max_new_tokens:
-            ctx = idx if idx.size(1) <= block else idx[:, -block:]
-            logits, _ = self.model(ctx)
-            last_h = self.model._last_hidden
-            main_row = logits[:, -1, :]
-            token_1 = draw(main_row)
-            draft_tokens, draft_rows = [token_1], [main_row]
-            prev_emb = self.model.transformer.wte(token_1)
-            for mtp_mod in self.model.mtp_modules:
-                h_mtp = mtp_mod(last_h[:, -1:, :], prev_emb)
-                row = self.model.lm_head(h_mtp[:, -1, :])
-                tok = draw(row)
-                draft_tokens.append(tok)
-                draft_rows.append(row)
-                prev_emb = self.model.transformer.wte(tok)
+        def main_forward(x):
+            logits, _ = self.model(x)
+            return logits[:, -1, :], self.model._last_hidden[:, -1:, :]
 
-            idx = torch.cat([idx, token_1], dim=1)
-            generated += 1
-            if generated >= max_new_tokens:
+        while True:
+            act = [b for b in range(n) if active[b]]
+            if not act:
                 break
-            K = len(draft_tokens) - 1
-            if K > 0:
-                verify_idx = torch.cat([idx, torch.cat(draft_tokens[1:], dim=1)], dim=1)
-                if verify_idx.size(1) > block:
-                    verify_idx = verify_idx[:, -block:]
-                verify_logits = self.model.full_logits(verify_idx)
-                prompt_len = idx.size(1)
-                offset = verify_idx.size(1) - (prompt_len + K)
-                first = prompt_len - 1 + offset
-                if first < 0 or first + K >= verify_logits.size(1):
-                    # fewer verify positions than drafts (the context window cut them)
-                    if idx.size(1) >= block:
-                        break
-                    continue
+            res = _grouped(main_forward, [s if s.numel() <= block else s[-block:] for s in (seqs[b] for b in act)])
+            main_rows = torch.stack([r[0] for r in res])
+            last_h = torch.stack([r[1] for r in res])            # [A, 1, D]
+            us: list = []
+            token_1 = draw(main_rows, us)
+            toks, rows = [token_1], [main_rows]
+            prev_emb = self.model.transformer.wte(token_1.view(-1, 1))
+            for mtp_mod in self.model.mtp_modules:
+                h_mtp = mtp_mod(last_h, prev_emb)
+                row = self.model.lm_head(h_mtp[:, -1, :])
+                tok = draw(row, us)
+                toks.append(tok)
+                rows.append(row)
+                prev_emb = self.model.transformer.wte(tok.view(-1, 1))
+            drafts = torch.stack(toks[1:], dim=1)                  # [A, K]
+            K = drafts.size(1)
+            rec = {"seqs": act, "u_draft": torch.stack(us, dim=1), "token_1": token_1, "draft_tokens": drafts,
+                   "verified": []}
+            go = []
+            for i, b in enumerate(act):
+                seqs[b] = torch.cat([seqs[b], token_1[i:i + 1].to(seqs[b].dtype)])
+                generated[b] += 1
+                if generated[b] >= max_new_tokens:
+                    active[b] = False
+                else:
+                    go.append(i)
+            vctx = [torch.cat([seqs[act[i]], drafts[i].to(seqs[act[i]].dtype)]) for i in go]
+            vctx = [c if c.numel() <= block else c[-block:] for c in vctx]
+            full = _grouped(lambda x: self.model.full_logits(x), vctx)
+            rows_t, ok = [], []
+            for j, i in enumerate(go):
+                L = vctx[j].numel()
+                first = seqs[act[i]].numel() - 1 + (L - (seqs[act[i]].numel() + K))
+                if first < 0 or first + K >= full[j].size(0):
+                    continue   # fewer verify positions than drafts (the context window cut them)
                 # positions first .. first + K - 1 verify drafts 1..K; position
                 # first + K would be the bonus, which this scheme does not draw
-                out = speculative_verify(verify_logits[:, first:first + K + 1, :].contiguous(),
-                                         torch.stack(draft_rows[1:], dim=1).to(verify_logits.dtype),
-                                         torch.cat(draft_tokens[1:], dim=1), temperature=T, top_k=k or None,
-                                         generator=generator)
-                n = int(out.n_accepted[0])
-                new = out.tokens[0, : (n if n == K else n + 1)]
-                new = new[: max_new_tokens - generated]
-                idx = torch.cat([idx, new.view(1, -1)], dim=1)
-                generated += new.numel()
-            if idx.size(1) >= block:
-                break
-        return idx
+                rows_t.append(full[j][first:first + K + 1])
+                ok.append(i)
+            rec["verified"] = ok
+            if ok:
+                sel = torch.tensor(ok, device=dev)
+                d_rows = torch.stack(rows[1:], dim=1)[sel].to(rows_t[0].dtype).contiguous()
+                u_acc = torch.rand(len(ok), K, device=dev, generator=generator)
+                u_res = torch.rand(len(ok), device=dev, generator=generator)
+                out = speculative_verify(torch.stack(rows_t), d_rows, drafts[sel].contiguous(), temperature=T,
+                                         top_k=k or None, u_accept=u_acc, u_resample=u_res, return_ratio=False)
+                n_acc = out.n_accepted.tolist()
+                otoks = out.tokens.tolist()
+                rec.update(u_accept=u_acc, u_resample=u_res, n_accepted=n_acc, tokens=otoks)
+                for j, i in enumerate(ok):
+                    b = act[i]
+                    na = n_acc[j]
+                    new = otoks[j][: (na if na == K else na + 1)][: max_new_tokens - generated[b]]
+                    seqs[b] = torch.cat([seqs[b], torch.tensor(new, dtype=seqs[b].dtype, device=dev)])
+                    generated[b] += len(new)
+                    if generated[b] >= max_new_tokens:
+                        active[b] = False
+            for b in act:
+                if seqs[b].numel() >= block:
+                    active[b] = False
+            if trace is not None:
+                trace.append(rec)
+        return _result(seqs, single)
