@@ -347,6 +347,110 @@ def bench_rowstats(args, dev) -> int:
     return 0
 
 
+def bench_lmhead(args, dev) -> int:
+    """The decode step's lm_head with the sampler in its epilogue
+    (lmhead_bf16_<B>x<D>x<V>): one step = LmHeadPlan.launch() (prep, sampled
+    bound, MFMA GEMM with the candidate epilogue, pick) for B rows of
+    D-dimensional bf16 hidden states against a V x D bf16 weight, per-row
+    top-k 1..64 with temperature, top-p, min-p and penalty.  Reported beside
+    it: the unfused step (torch.matmul into [B, V] bf16 logits, then
+    fl_sample over them)."""
+    import torch
+
+    from rl_project_amd.lmhead import LmHeadPlan
+    from rl_project_amd.sampling import SamplerPlan
+
+    parts = args.workload.split("_")
+    B, D, V = (int(v) for v in parts[2].split("x"))
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(B, D, generator=g, device=dev).to(torch.bfloat16)
+    W = (torch.randn(V, D, generator=g, device=dev) * (2.5 / D ** 0.5)).to(torch.bfloat16)
+    gc = torch.Generator().manual_seed(1)
+    kw = dict(temperature=torch.rand(B, generator=gc) * 1.4 + 0.1,
+              top_k=torch.tensor([1, 5, 20, 50, 64], dtype=torch.int32)[torch.randint(0, 5, (B,), generator=gc)],
+              top_p=torch.where(torch.rand(B, generator=gc) < 0.6, torch.rand(B, generator=gc) * 0.5 + 0.5,
+                                torch.ones(B)),
+              min_p=torch.where(torch.rand(B, generator=gc) < 0.3, torch.full((B,), 0.05), torch.zeros(B)),
+              repetition_penalty=torch.rand(B, generator=gc) * 0.3 + 1.0,
+              history=torch.randint(0, V, (B, 2048), generator=gc, dtype=torch.int32),
+              uniforms=torch.rand(B, generator=gc))
+    kd = {k: v.to(dev) for k, v in kw.items()}
+    plan = LmHeadPlan(h, W, **kd)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        plan.launch()
+    torch.cuda.synchronize(dev)
+    if int((plan.status != 0).sum()):
+        print(f"rows failed: status {plan.status.tolist()[:16]}", file=sys.stderr)
+        return 1
+    K = args.steps
+    step_ms, wall = _timed_region(torch, dev, stream, K, lambda k: plan.launch())
+    durs = _isolated_launches(torch, dev, stream, lambda k: plan.launch())
+    # the unfused step: GEMM into logits, then fl_sample
+    logits = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
+    splan = SamplerPlan(logits, **kd)
+
+    def unfused(k):
+        torch.matmul(h, W.t(), out=logits)
+        splan.launch()
+    for _ in range(args.warmup):
+        unfused(0)
+    unf_ms, _ = _timed_region(torch, dev, stream, K, unfused)
+    gemm_ms, _ = _timed_region(torch, dev, stream, K, lambda k: torch.matmul(h, W.t(), out=logits))
+    alg_bytes = V * D * 2 + B * D * 2 + B * 16
+    achieved = alg_bytes / (step_ms * 1e-3) / 1e9
+    flops = 2.0 * B * D * V
+    result = {
+        "metric": f"decode steps/sec: lm_head + sampling of {B} rows, D={D}, V={V} (bf16), no [B,V] logits in HBM",
+        "value": K / wall, "unit": "steps/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / K, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": args.workload, "batch": B, "dim": D, "vocab": V, "history": 2048,
+                   "tokens_per_s": B * K / wall},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(args.workload),
+                     "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
+                     "isolated_step_ms_p10": durs[len(durs) // 10],
+                     "isolated_step_ms_p90": durs[(9 * len(durs)) // 10],
+                     "kernel": "k_lm_prep + k_lm_gemm<sample> + k_lm_thresh + k_lm_gemm + k_lm_pick",
+                     "mfma_tflops": flops / (step_ms * 1e-3) / 1e12, "mfma_peak_tflops": 2500.0},
+        "unfused": {"ms_per_step": unf_ms, "matmul_ms": gemm_ms,
+                    "note": "torch.matmul(h, W.T) into [B, V] bf16 logits, then fl_sample (SamplerPlan)"},
+    }
+    if not args.no_cpu_baseline:
+        # the reference's step on the host: the float32 product rounded to bf16
+        # logits, then the oracle's per-row filters and selection; the GPU's own
+        # logits and tokens checked against the oracle
+        from oracle import classify as C
+        from oracle import sampler_oracle as O
+        pl = LmHeadPlan(h, W, return_logits=True, **kd)
+        pl.launch()
+        torch.cuda.synchronize(dev)
+        x = pl.logits.cpu()
+        params = [O.RowParams(temperature=float(kw["temperature"][b]), top_k=int(kw["top_k"][b]),
+                              top_p=float(kw["top_p"][b]), min_p=float(kw["min_p"][b]),
+                              repetition_penalty=float(kw["repetition_penalty"][b]),
+                              history=kw["history"][b].tolist()) for b in range(B)]
+        ref = O.sample_rows(x, params, kw["uniforms"].tolist(), want_filtered=True)
+        toks = pl.tokens.cpu().tolist()
+        verdicts = [C.classify_row(x[b], params[b], float(kw["uniforms"][b]), ~torch.isneginf(ref[b].filtered.float()),
+                                   ref[b].token, None, toks[b]) for b in range(B)]
+        result["parity"] = C.summarise(verdicts)
+        hc, Wc = h.float().cpu(), W.float().cpu()
+        steps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or steps == 0:
+            xl = (hc @ Wc.t()).to(torch.bfloat16)
+            O.sample_rows(xl, params, kw["uniforms"].tolist(), want_filtered=False)
+            steps += 1
+        dt_cpu = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": steps / dt_cpu, "unit": "steps/s", "cores": torch.get_num_threads(),
+                                  "kind": "port", "sample": f"{steps} steps of float32 torch.matmul + the oracle's "
+                                  f"per-row sampling (torch {torch.__version__} CPU, {torch.get_num_threads()} "
+                                  f"threads), {dt_cpu:.1f} s"}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -389,6 +493,8 @@ def main() -> int:
         return bench_spec(args, dev)
     if args.workload.startswith("rowstats_"):
         return bench_rowstats(args, dev)
+    if args.workload.startswith("lmhead_"):
+        return bench_lmhead(args, dev)
     w = workloads.make(args.workload, seed=0)
     batch_bytes = w.logits.numel() * w.logits.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))

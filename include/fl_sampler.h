@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FL_ABI_VERSION 4
+#define FL_ABI_VERSION 5
 
 enum fl_dtype { FL_DTYPE_F32 = 0, FL_DTYPE_BF16 = 1, FL_DTYPE_F16 = 2 };
 
@@ -273,6 +273,67 @@ typedef struct fl_row_stats_args {
 #define FL_MAX_VOCAB_STATS (1 << 24)  /* elements per row for fl_row_stats */
 
 int fl_row_stats(const fl_row_stats_args* args, void* stream);
+
+/*
+ * lm_head with the sampler fused into its epilogue, for decode steps whose
+ * rows all use top-k (reference: the step's logits come from
+ * lm_head(h[:, -1, :]), transformer/model.py:190 and :201, and are sampled by
+ * sampling.py:16-61 as fl_sample does).
+ *
+ *   logits[b, v] = bf16(sum_d hidden[b, d] * weight[v, d])   (fp32 accumulation)
+ *
+ * is computed on the matrix cores; each logit goes through soft-cap, the
+ * repetition penalty (rows' history ids) and the temperature in the
+ * epilogue, and only the values that can be among a row's top_k largest are
+ * written (as candidates to the workspace), never the [batch, vocab] logits.
+ * A second kernel samples each row from its candidates with fl_sample's
+ * rules (top-k with ties, min-p, top-p, inverse-CDF or greedy selection,
+ * log-probability).  hidden [batch, dim] (row stride ld_hidden) and weight
+ * [vocab, dim] (rows contiguous) are bf16; batch <= FL_LM_HEAD_MAX_BATCH, dim a
+ * multiple of 64.  Per-row parameters as in fl_sample_args; top_k must lie in
+ * 1 .. FL_LM_HEAD_MAX_TOPK.  A row whose top_k is outside that range, or whose
+ * candidates exceed FL_LM_HEAD_MAX_CAND (more than that many values tie above
+ * the threshold), reports FL_ROW_LIMIT and no token: sample it with fl_sample
+ * over out_logits.  out_logits (NULL, or [batch, vocab] bf16) receives the
+ * logits as computed, for such rows and for checks.  The workspace
+ * (fl_lm_head_workspace_bytes) is the caller's scratch: calls that overlap in
+ * time must not share one.
+ */
+#define FL_LM_HEAD_MAX_BATCH 64
+#define FL_LM_HEAD_MAX_TOPK 64
+#define FL_LM_HEAD_MAX_CAND 4096
+typedef struct fl_lm_head_args {
+  uint32_t struct_size;
+  int32_t dtype;                   /* FL_DTYPE_BF16 */
+  const void* hidden;              /* [batch, dim], row stride ld_hidden */
+  const void* weight;              /* [vocab, dim] */
+  int64_t batch;
+  int64_t dim;
+  int64_t vocab;
+  int64_t ld_hidden;
+  const float* temperature;        /* [batch] */
+  const int32_t* top_k;            /* [batch] */
+  const float* top_p;              /* [batch] */
+  const float* min_p;              /* [batch] */
+  const float* repetition_penalty; /* [batch] or NULL */
+  const int32_t* hist_ids;         /* as fl_sample_args, or NULL */
+  const int32_t* hist_len;
+  int64_t hist_ld;
+  float softcap;
+  const float* uniforms;           /* [batch] */
+  int64_t* out_token;              /* [batch] */
+  int32_t* out_status;             /* [batch] */
+  float* out_logprob;              /* [batch] or NULL */
+  void* out_logits;                /* [batch, vocab] bf16 or NULL */
+  void* workspace;
+  int64_t workspace_bytes;
+} fl_lm_head_args;
+
+int fl_lm_head_sample(const fl_lm_head_args* args, void* stream);
+
+/* Bytes of workspace fl_lm_head_sample needs for `batch` rows of `vocab`
+ * values (no counterpart in the reference). */
+int fl_lm_head_workspace_bytes(int64_t batch, int64_t vocab, size_t* out_bytes);
 
 /* Thread-local description of the last error returned on this thread. */
 const char* fl_last_error(void);

@@ -21,6 +21,7 @@ from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, desc
 from .speculative import MTPSpeculativeGenerator, SpeculativeGenerator, SpecOutput, SpecPlan, speculative_verify
 from .engine import BatchedSampler
 from .logprobs import RowStats, entropy_from_logits, kl_full_distribution, row_stats, token_logprobs_from_logits
+from .lmhead import LmHeadOutput, LmHeadPlan, lm_head_sample
 
 __all__ = [
     "apply_sampling_filters", "sample_from_logits", "generate_tokens",
@@ -28,4 +29,5 @@ __all__ = [
     "speculative_verify", "SpeculativeGenerator", "MTPSpeculativeGenerator", "SpecOutput", "SpecPlan",
     "BatchedSampler", "row_stats", "RowStats", "token_logprobs_from_logits", "entropy_from_logits", "kl_full_distribution",
     "SamplingParams", "GenerationSettings", "SamplingParamsError",
+    "lm_head_sample", "LmHeadPlan", "LmHeadOutput",
 ]

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflsampler.so")
 
-FL_ABI_VERSION = 4
+FL_ABI_VERSION = 5
 FL_DTYPE_F32, FL_DTYPE_BF16, FL_DTYPE_F16 = 0, 1, 2
 FL_OK, FL_EIO, FL_EINVAL, FL_ENOTSUP = 0, -5, -22, -95
 FL_ROW_OK, FL_ROW_NAN, FL_ROW_INF, FL_ROW_BAD_HISTORY, FL_ROW_LIMIT, FL_ROW_ALL_MASKED = 0, 1, 2, 4, 8, 16
@@ -76,6 +76,23 @@ class RowStatsArgs(ctypes.Structure):
     ]
 
 
+class LmHeadArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32), ("dtype", ctypes.c_int32),
+        ("hidden", _p), ("weight", _p),
+        ("batch", ctypes.c_int64), ("dim", ctypes.c_int64), ("vocab", ctypes.c_int64), ("ld_hidden", ctypes.c_int64),
+        ("temperature", _p), ("top_k", _p), ("top_p", _p), ("min_p", _p), ("repetition_penalty", _p),
+        ("hist_ids", _p), ("hist_len", _p), ("hist_ld", ctypes.c_int64), ("softcap", ctypes.c_float),
+        ("uniforms", _p), ("out_token", _p), ("out_status", _p), ("out_logprob", _p), ("out_logits", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+FL_LM_HEAD_MAX_BATCH = 64
+FL_LM_HEAD_MAX_TOPK = 64
+FL_LM_HEAD_MAX_CAND = 4096
+
+
 # fl_row_desc: {float y_cut; int32 idx_cut; float shift; float inv_mass; double mass; int32 status; int32 n_kept}
 ROW_DESC_BYTES = 32
 
@@ -112,6 +129,10 @@ def lib() -> ctypes.CDLL:
     handle.fl_spec_verify_static.restype = ctypes.c_int
     handle.fl_spec_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
     handle.fl_spec_workspace_bytes.restype = ctypes.c_int
+    handle.fl_lm_head_sample.argtypes = [ctypes.POINTER(LmHeadArgs), _p]
+    handle.fl_lm_head_sample.restype = ctypes.c_int
+    handle.fl_lm_head_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
+    handle.fl_lm_head_workspace_bytes.restype = ctypes.c_int
     handle.fl_row_stats.argtypes = [ctypes.POINTER(RowStatsArgs), _p]
     handle.fl_row_stats.restype = ctypes.c_int
     if handle.fl_abi_version() != FL_ABI_VERSION:
@@ -136,5 +157,5 @@ def stream_handle(device: torch.device) -> int:
 
 
 EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_verify_static",
-                    "fl_spec_workspace_bytes", "fl_row_stats",
+                    "fl_spec_workspace_bytes", "fl_lm_head_sample", "fl_lm_head_workspace_bytes", "fl_row_stats",
                     "fl_last_error", "fl_abi_version")

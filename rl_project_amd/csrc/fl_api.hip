@@ -171,6 +171,50 @@ int fl_row_stats(const fl_row_stats_args* a, void* stream) {
   return check_launch(e, "fl_row_stats");
 }
 
+int fl_lm_head_workspace_bytes(int64_t batch, int64_t vocab, size_t* out_bytes) {
+  if (out_bytes == nullptr) return fail(FL_EINVAL, "fl_lm_head_workspace_bytes: out_bytes is NULL");
+  if (batch < 0 || batch > FL_LM_HEAD_MAX_BATCH || vocab < 1 || vocab > FL_MAX_VOCAB_16)
+    return fail(FL_EINVAL, "fl_lm_head_workspace_bytes: bad batch %lld or vocab %lld", static_cast<long long>(batch),
+                static_cast<long long>(vocab));
+  *out_bytes = fl::lm_head_workspace_bytes(batch, vocab);
+  return ok();
+}
+
+int fl_lm_head_sample(const fl_lm_head_args* a, void* stream) {
+  const char* fn = "fl_lm_head_sample";
+  if (a == nullptr) return fail(FL_EINVAL, "%s: args is NULL", fn);
+  if (a->struct_size != sizeof(fl_lm_head_args)) return fail(FL_EINVAL, "%s: struct_size mismatch", fn);
+  if (a->dtype != FL_DTYPE_BF16) return fail(FL_ENOTSUP, "%s: dtype %d (bf16 only)", fn, a->dtype);
+  if (a->batch < 0 || a->vocab < 1 || a->dim < 64 || a->dim % 64 != 0 || a->ld_hidden < a->dim)
+    return fail(FL_EINVAL, "%s: bad shape batch=%lld dim=%lld vocab=%lld ld_hidden=%lld (dim a multiple of 64)", fn,
+                static_cast<long long>(a->batch), static_cast<long long>(a->dim), static_cast<long long>(a->vocab),
+                static_cast<long long>(a->ld_hidden));
+  if (a->batch > FL_LM_HEAD_MAX_BATCH || a->vocab > FL_MAX_VOCAB_16 || a->dim > 16384 ||
+      a->batch * a->ld_hidden > (1ll << 29))
+    return fail(FL_ENOTSUP, "%s: batch %lld, vocab %lld or dim %lld beyond the library's limits (%d, %d, 16384)", fn,
+                static_cast<long long>(a->batch), static_cast<long long>(a->vocab), static_cast<long long>(a->dim),
+                FL_LM_HEAD_MAX_BATCH, FL_MAX_VOCAB_16);
+  if (!std::isfinite(a->softcap) || a->softcap < 0.0f)
+    return fail(FL_EINVAL, "%s: softcap must be finite and >= 0", fn);
+  if (a->batch == 0) return ok();
+  if (!a->hidden || !a->weight || !a->temperature || !a->top_k || !a->top_p || !a->min_p || !a->uniforms ||
+      !a->out_token || !a->out_status)
+    return fail(FL_EINVAL, "%s: a required pointer is NULL", fn);
+  if (a->hist_ids != nullptr && (a->hist_len == nullptr || a->hist_ld < 0))
+    return fail(FL_EINVAL, "%s: hist_ids needs hist_len and hist_ld >= 0", fn);
+  if (a->workspace == nullptr || a->workspace_bytes < 0 ||
+      static_cast<size_t>(a->workspace_bytes) < fl::lm_head_workspace_bytes(a->batch, a->vocab))
+    return fail(FL_EINVAL, "%s: workspace of %lld bytes, %zu needed", fn, static_cast<long long>(a->workspace_bytes),
+                fl::lm_head_workspace_bytes(a->batch, a->vocab));
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+    return fail(FL_EINVAL, "%s: workspace not 256-byte aligned", fn);
+  if ((reinterpret_cast<uintptr_t>(a->hidden) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a->weight) & 15u) != 0 ||
+      (a->ld_hidden % 8) != 0)
+    return fail(FL_EINVAL, "%s: hidden and weight must be 16-byte aligned (ld_hidden a multiple of 8)", fn);
+  const hipError_t e = fl::launch_lm_head(*a, static_cast<hipStream_t>(stream));
+  return check_launch(e, fn);
+}
+
 int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes) {
   if (out_bytes == nullptr) return fail(FL_EINVAL, "fl_spec_workspace_bytes: out_bytes is NULL");
   if (batch < 0 || batch > 0x7fffffff)

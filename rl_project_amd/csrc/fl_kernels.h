@@ -24,4 +24,8 @@ hipError_t launch_spec_verify_static(const fl_spec_args& a, hipStream_t s);
 size_t spec_static_scratch_bytes();
 hipError_t launch_row_stats(const fl_row_stats_args& a, hipStream_t s);
 
+// lm_head GEMM with the sampler in its epilogue (prep, gemm, pick).
+hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s);
+size_t lm_head_workspace_bytes(int64_t batch, int64_t vocab);
+
 }  // namespace fl

@@ -1,0 +1,613 @@
+// lm_head with the sampler in its epilogue (reference: the decode step's
+// logits, lm_head(h[:, -1, :]) at transformer/model.py:190 and :201, sampled
+// by generation/sampling.py:16-61), for rows that all use top-k.
+//
+//   prep    one work-group per row: the row's history bitmap (one bit per
+//           vocabulary id, which also de-duplicates the ids) and counters;
+//   sample  the gemm below over every S-th vocabulary row (ns <= 8192 rows,
+//           S = ceil(vocab / 8192)), in tiles of 64 rows so that many work-groups
+//           share the work; it stores each sampled value's order key.  A
+//           logit's value does not depend on its tile: the same MFMA chain
+//           over the same dim order produces it in both gemms;
+//   thresh  one work-group per row: the k-th largest sampled key.  The sampled
+//           values are a subset of the row's, so at least k of the row's values
+//           reach it: a lower bound of the row's k-th largest value;
+//   gemm    logits = hidden · weightᵀ on the matrix cores
+//           (v_mfma_f32_16x16x32_bf16, fp32 accumulation), one work-group per
+//           256 vocabulary rows and every batch row.  The weight streams from
+//           HBM once, straight into a three-deep register ring; the hidden
+//           states go through LDS two stages ahead.  Epilogue per logit: bf16
+//           rounding (the logits tensor the reference would hold), then
+//           soft-cap, penalty and temperature as fl_sample applies them; the
+//           values at or above the row's bound are appended to the row's
+//           candidates (about k·S of them);
+//   pick    one work-group per row: the exact k-th largest candidate by a
+//           two-pass radix select, the kept values (ties kept) sorted, then
+//           min-p, top-p and the draw with fl_sample's arithmetic.
+//
+// Traffic: the weight once plus its sampled rows (1/S of it), and the hidden
+// states; the [batch, vocab] logits are neither written nor read back.
+#include <type_traits>
+
+#include "fl_device.h"
+#include "fl_kernels.h"
+
+namespace fl {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int LM_NT = 256;                 // threads of the gemm and pick work-groups
+constexpr int LM_NTILE = 256;              // vocabulary rows per gemm tile (64 per wave)
+constexpr int LM_KC = 64;                  // dim per pipeline stage (two MFMA steps of 32)
+constexpr int LM_AST = LM_KC + 8;          // LDS row stride of a hidden-state stage, bf16 elements
+constexpr int LM_NST = 3;                  // weight stages in flight per wave
+constexpr int LM_NSAMPLE = 8192;           // sampled vocabulary rows (at most)
+constexpr int LM_CAP = FL_LM_HEAD_MAX_CAND;
+
+// Ascending order key of a 16-bit float pattern: larger value, larger key;
+// 0 only for the all-ones NaN pattern (the epilogue maps every NaN to 0).
+__device__ __forceinline__ uint32_t asc16(uint32_t bits) { return 0xFFFFu - order16(bits); }
+__device__ __forceinline__ uint32_t bits_of_asc16(uint32_t k) { return bits_of_order16(0xFFFFu - k); }
+
+struct LmWs {
+  uint32_t* thr;    // [batch] the row's bound (asc16 key; 0: none)
+  uint32_t* cnt;    // [batch] candidates appended
+  uint32_t* stat;   // [batch] FL_ROW_* bits found by prep and gemm
+  uint32_t* bits;   // [batch, bw] history bitmap
+  uint16_t* skey;   // [batch, ns] keys of the sampled rows (entry e: vocabulary row e·S)
+  uint64_t* cand;   // [batch, LM_CAP] (key << 32) | ~vocabulary index
+  int bw;
+  int stride;       // S
+  int ns;
+};
+
+__host__ __device__ inline int lm_stride(int64_t vocab) {  // ceil(vocab / 8192): ns <= 8192
+  return static_cast<int>((vocab + LM_NSAMPLE - 1) / LM_NSAMPLE);
+}
+__host__ __device__ inline int lm_ns(int64_t vocab) {
+  return static_cast<int>((vocab + lm_stride(vocab) - 1) / lm_stride(vocab));
+}
+__host__ __device__ inline size_t lm_align(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+__host__ __device__ inline size_t lm_ws_bytes(int64_t batch, int64_t vocab) {
+  const size_t B = static_cast<size_t>(batch), bw = static_cast<size_t>((vocab + 31) / 32);
+  return 3 * lm_align(4 * B) + lm_align(4 * B * bw) + lm_align(2 * B * static_cast<size_t>(lm_ns(vocab))) +
+         8 * B * LM_CAP;
+}
+inline LmWs lm_ws(void* p, int64_t batch, int64_t vocab) {
+  const size_t B = static_cast<size_t>(batch);
+  char* q = static_cast<char*>(p);
+  LmWs w;
+  w.bw = static_cast<int>((vocab + 31) / 32);
+  w.stride = lm_stride(vocab);
+  w.ns = lm_ns(vocab);
+  size_t off = 0;
+  w.thr = reinterpret_cast<uint32_t*>(q + off);
+  off += lm_align(4 * B);
+  w.cnt = reinterpret_cast<uint32_t*>(q + off);
+  off += lm_align(4 * B);
+  w.stat = reinterpret_cast<uint32_t*>(q + off);
+  off += lm_align(4 * B);
+  w.bits = reinterpret_cast<uint32_t*>(q + off);
+  off += lm_align(4 * B * w.bw);
+  w.skey = reinterpret_cast<uint16_t*>(q + off);
+  off += lm_align(2 * B * static_cast<size_t>(w.ns));
+  w.cand = reinterpret_cast<uint64_t*>(q + off);
+  return w;
+}
+
+__device__ __forceinline__ bool row_penalised(const fl_lm_head_args& a, int b) {
+  return a.repetition_penalty != nullptr && a.hist_ids != nullptr && a.hist_len != nullptr &&
+         a.repetition_penalty[b] != 1.0f;
+}
+
+// The k-th largest of n 16-bit keys (0 when n < k), by one wave: two passes of a 256-bin histogram (high byte, then the
+// low byte within the chosen high byte).  hist: 256 words of LDS for this wave.
+template <class KeyAt>
+__device__ uint32_t wave_kth_key(int n, int k, uint32_t* hist, KeyAt&& key_at) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  uint32_t prefix = 0;   // high byte, once chosen
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hist[lane + WAVE * q] = 0u;
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < n; i += WAVE) {
+      const uint32_t key = key_at(i);
+      if (pass == 0) atomicAdd(&hist[key >> 8], 1u);
+      else if ((key >> 8) == prefix) atomicAdd(&hist[key & 0xFFu], 1u);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // bins from the top: lane holds bins 255 - 4 lane .. 252 - 4 lane
+    uint32_t c4[4], s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = hist[255 - 4 * lane - q];
+      s += c4[q];
+    }
+    const uint32_t incl = wave_incl_scan(s);
+    const uint32_t before = incl - s;   // keys in higher bins
+    // the bin where the count from the top reaches k
+    int bin = -1;
+    uint32_t run = before;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (bin < 0 && run + c4[q] >= static_cast<uint32_t>(k)) bin = 255 - 4 * lane - q;
+      if (bin < 0) run += c4[q];
+    }
+    const uint64_t m = __ballot(bin >= 0);
+    if (m == 0) return 0u;   // fewer than k keys
+    const int src = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const uint32_t chosen = static_cast<uint32_t>(__shfl(bin, src, WAVE));
+    const uint32_t above = static_cast<uint32_t>(__shfl(static_cast<int>(run), src, WAVE));
+    k -= static_cast<int>(above);
+    if (pass == 0) prefix = chosen;
+    else return (prefix << 8) | chosen;
+    __builtin_amdgcn_wave_barrier();
+  }
+  return 0u;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- prep
+__global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs ws) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  uint32_t* bits = ws.bits + static_cast<size_t>(b) * ws.bw;
+  for (int i = tid; i < ws.bw; i += LM_NT) bits[i] = 0u;
+  if (tid == 0) {
+    ws.thr[b] = 0u;
+    ws.cnt[b] = 0u;
+    ws.stat[b] = 0u;
+  }
+  __syncthreads();  // (the bitmap's zeros reach memory before the atomics below)
+  if (!row_penalised(a, b)) return;
+  int H = a.hist_len[b];
+  if (H > FL_MAX_HISTORY) {
+    if (tid == 0) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_LIMIT));
+    return;
+  }
+  if (a.hist_ld > 0 && H > a.hist_ld) {  // (a length past its row: the row's ids only)
+    if (tid == 0) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
+    H = static_cast<int>(a.hist_ld);
+  }
+  const int32_t* hid = a.hist_ids + static_cast<int64_t>(b) * a.hist_ld;
+  for (int i = tid; i < H; i += LM_NT) {
+    const int id = hid[i];
+    if (id < 0 || id >= a.vocab) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
+    else atomicOr(&bits[id >> 5], 1u << (id & 31));
+  }
+}
+
+// ---------------------------------------------------------------- gemm + epilogue
+// MB: 16-row blocks of the batch (1, 2 or 4).  SC: a soft-cap.  SAMPLE: the
+// sampled rows (16 per wave, 64 per work-group), keys stored; otherwise 64
+// contiguous vocabulary rows per wave, 256 per work-group, candidates
+// appended.  Each 16 x 16 block of logits is one wave's MFMA chain over the
+// dim in the same order in both forms, so a sampled value equals the main
+// gemm's value of the same logit bit for bit.
+template <int MB, bool SC, bool SAMPLE>
+__global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs ws) {
+  constexpr int NB = SAMPLE ? 1 : 4;        // 16-row weight blocks per wave
+  constexpr int TILE = 16 * NB * (LM_NT / WAVE);
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][16 * MB * LM_AST];
+  __shared__ uint16_t sKey[SAMPLE ? 1 : 16 * MB][SAMPLE ? 1 : TILE];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
+  const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim), V = static_cast<int>(a.vocab);
+  const int S = SAMPLE ? ws.stride : 1;
+  const int nrows = SAMPLE ? ws.ns : V;     // tile entries (sampled rows, or vocabulary rows)
+  const int e0 = blockIdx.x * TILE;
+  const int l16 = lane & 15, l4 = lane >> 4;
+  const uint16_t* W = static_cast<const uint16_t*>(a.weight);
+  // hidden rows 0 .. B-1 (rows of the last block past B read zeros)
+  const __amdgpu_buffer_rsrc_t rh =
+      row_rsrc(a.hidden, 2u * static_cast<uint32_t>(B - 1) * static_cast<uint32_t>(a.ld_hidden) + 2u * D);
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // lane's weight fragment of block nb, step ks: tile entry 16 NB w + 16 nb +
+  // l16, vocabulary row (e0 + entry)·S (entries past the end read the last
+  // row; their results are dropped), dim k0 + 32 ks + 8 l4 .. +7
+  const uint16_t* wp[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int e = min(e0 + 16 * NB * w + 16 * nb + l16, nrows - 1);
+    wp[nb] = W + static_cast<int64_t>(e) * S * D + 8 * l4;
+  }
+  // hidden-state stage: 16 MB rows x 64 columns = 128 MB pieces of 16 bytes
+  constexpr int APIECES = (16 * MB * LM_KC / 8 + LM_NT - 1) / LM_NT;
+  auto load_a = [&](uint4 (&ap)[APIECES], int k0) {
+#pragma unroll
+    for (int s = 0; s < APIECES; ++s) {
+      const int idx = tid + LM_NT * s;
+      const int row = idx >> 3, seg = idx & 7;
+      const bool in = row < 16 * MB && row < B;
+      ap[s] = in ? buf_load16(rh, 2u * (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * seg), 0u)
+                 : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_a = [&](const uint4 (&ap)[APIECES], int st) {
+#pragma unroll
+    for (int s = 0; s < APIECES; ++s) {
+      const int idx = tid + LM_NT * s;
+      const int row = idx >> 3, seg = idx & 7;
+      if (row < 16 * MB) *reinterpret_cast<uint4*>(&sA[st][row * LM_AST + 8 * seg]) = ap[s];
+    }
+  };
+  auto load_w = [&](uint4 (&wf)[2][NB], int k0) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wf[ks][nb] = *reinterpret_cast<const uint4*>(wp[nb] + k0 + 32 * ks);
+  };
+  auto mfma_stage = [&](int st, const uint4 (&wf)[2][NB]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(&sA[st][(16 * mb + l16) * LM_AST + 32 * ks + 8 * l4]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8, wf[ks][nb]),
+                                                                acc[mb][nb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Pipeline: iteration `it` stores the hidden stage it + 1 (loaded during
+  // it - 1) into LDS, loads stage it + 2, multiplies stage it, then refills
+  // its weight slot with stage it + LM_NST.
+  const int NIT = D / LM_KC;
+  uint4 an[APIECES];
+  uint4 wr[LM_NST][2][NB];
+  load_a(an, 0);
+#pragma unroll
+  for (int u = 0; u < LM_NST; ++u)
+    if (u < NIT) load_w(wr[u], u * LM_KC);
+  store_a(an, 0);
+  if (NIT > 1) load_a(an, LM_KC);
+  __syncthreads();
+  for (int it0 = 0; it0 < NIT; it0 += LM_NST) {
+#pragma unroll
+    for (int u = 0; u < LM_NST; ++u) {
+      const int it = it0 + u;
+      if (it < NIT) {
+        if (it + 1 < NIT) store_a(an, (it + 1) & 1);
+        if (it + 2 < NIT) load_a(an, (it + 2) * LM_KC);
+        mfma_stage(it & 1, wr[u]);
+        if (it + LM_NST < NIT) load_w(wr[u], (it + LM_NST) * LM_KC);
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---------------- epilogue: values and their keys
+  // lane holds (m, tile entry c) = (16 mb + 4 l4 + r, 16 NB w + 16 nb + l16) in
+  // acc[mb][nb][r]; its vocabulary row is (e0 + c)·S
+  const float cap = a.softcap;
+  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+      const bool row_ok = m < B;
+      const int mc = row_ok ? m : 0;
+      const float T = a.temperature[mc];
+      const float RT = T > 0.0f ? 1.0f / T : 0.0f;
+      const bool pen = row_ok && row_penalised(a, mc);
+      const float RP = pen ? a.repetition_penalty[mc] : 1.0f;
+      const uint32_t* hb = ws.bits + static_cast<size_t>(mc) * ws.bw;
+      uint32_t flags = 0;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int c = 16 * NB * w + 16 * nb + l16;
+        const int e = e0 + c;
+        const int n = e * S;
+        const bool ok = row_ok && e < nrows;
+        const uint32_t xb = BF16::from_f32(acc[mb][nb][r]);
+        if (!SAMPLE && out_logits != nullptr && ok) out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(xb);
+        float z = BF16::to_f32(xb);
+        if constexpr (SC) z = softcap_val<BF16>(z, cap);
+        if (pen && ok && ((hb[n >> 5] >> (n & 31)) & 1u)) z = penalty_val<BF16>(z, RP);
+        const float y = temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
+        const uint32_t yb = BF16::from_f32(y);
+        const bool nan = y != y;
+        const uint32_t key = (ok && !nan) ? asc16(yb) : 0u;
+        if constexpr (SAMPLE) {
+          if (ok) ws.skey[static_cast<size_t>(m) * ws.ns + e] = static_cast<uint16_t>(key);
+        } else {
+          flags |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
+          flags |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
+          sKey[m][c] = static_cast<uint16_t>(key);
+        }
+      }
+      if (!SAMPLE && flags) atomicOr(&ws.stat[m], flags);
+    }
+  }
+  if constexpr (!SAMPLE) {
+    __syncthreads();
+    // ---------------- per row: append the tile's values at or above the bound
+    const int rows = min(B, 16 * MB);
+    for (int m = w; m < rows; m += LM_NT / WAVE) {
+      const int K = a.top_k[m];
+      if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) continue;
+      const uint32_t thr = ws.thr[m];
+      uint64_t sel[4];
+      uint32_t k4[4];
+      int total = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        k4[q] = sKey[m][lane + WAVE * q];
+        sel[q] = __ballot(k4[q] != 0u && k4[q] >= thr);
+        total += __popcll(sel[q]);
+      }
+      if (total == 0) continue;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&ws.cnt[m], static_cast<uint32_t>(total));
+      base = static_cast<uint32_t>(__shfl(static_cast<int>(base), 0, WAVE));
+      uint64_t* cand = ws.cand + static_cast<size_t>(m) * LM_CAP;
+      const uint64_t below = (1ull << lane) - 1ull;
+      uint32_t pos = base;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if ((sel[q] >> lane) & 1ull) {
+          const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel[q] & below));
+          const uint32_t n = static_cast<uint32_t>(e0 + lane + WAVE * q);
+          if (p < static_cast<uint32_t>(LM_CAP)) cand[p] = (static_cast<uint64_t>(k4[q]) << 32) | static_cast<uint32_t>(~n);
+        }
+        pos += static_cast<uint32_t>(__popcll(sel[q]));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- thresh
+// The K-th largest of the row's sampled keys (0 when fewer than K were
+// sampled): the keys into LDS, then the radix select of wave 0.
+__global__ __launch_bounds__(LM_NT) void k_lm_thresh(const fl_lm_head_args a, LmWs ws) {
+  __shared__ uint16_t keys[LM_NSAMPLE];
+  __shared__ uint32_t hist[256];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int K = a.top_k[b];
+  if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) return;   // (the pick reports the row)
+  const uint16_t* src = ws.skey + static_cast<size_t>(b) * ws.ns;
+  for (int i = tid; i < ws.ns; i += LM_NT) keys[i] = src[i];
+  __syncthreads();
+  if (tid >= WAVE) return;
+  const uint32_t t = wave_kth_key(ws.ns, K, hist, [&](int i) { return static_cast<uint32_t>(keys[i]); });
+  if (tid == 0) ws.thr[b] = t;
+}
+
+// ---------------------------------------------------------------- pick
+namespace {
+// Descending bitonic sort of n (a power of two, 128 .. 1024) 64-bit keys in
+// LDS by the work-group.
+__device__ void lm_sort_desc(uint64_t* buf, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += LM_NT) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint64_t x = buf[i], y = buf[p];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            buf[i] = y;
+            buf[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+// The same for 64 keys, one per lane of a wave, through lane shuffles.
+__device__ uint64_t wave_sort_desc(uint64_t v) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  for (int k = 2; k <= WAVE; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t o = shfl_xor(v, j);
+      const bool desc = (lane & k) == 0, lower = (lane & j) == 0;
+      v = (lower == desc) ? (v > o ? v : o) : (v < o ? v : o);
+    }
+  }
+  return v;
+}
+constexpr int LM_KEEP = 1024;  // kept values (the k largest and their ties) a row may have
+}  // namespace
+
+__global__ __launch_bounds__(LM_NT) void k_lm_pick(const fl_lm_head_args a, LmWs ws) {
+  __shared__ uint64_t c[LM_CAP];      // the candidates
+  __shared__ uint64_t kept[LM_KEEP];  // the kept ones, sorted
+  __shared__ uint32_t sHist[256];
+  __shared__ uint32_t s_n, s_nk, s_kth;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (WAVE - 1);
+  uint32_t status = ws.stat[b];
+  const int K = a.top_k[b];
+  const uint32_t nc = ws.cnt[b];
+  if (K < 1 || K > FL_LM_HEAD_MAX_TOPK || nc > static_cast<uint32_t>(LM_CAP)) status |= FL_ROW_LIMIT;
+  if (tid == 0) {
+    s_n = 0;
+    s_nk = 0;
+  }
+  __syncthreads();
+  if (status == 0) {
+    const uint64_t* cand = ws.cand + static_cast<size_t>(b) * LM_CAP;
+    for (uint32_t i = tid; i < nc; i += LM_NT) c[i] = cand[i];
+    if (tid == 0) s_n = nc;
+  }
+  __syncthreads();
+  const uint32_t n = s_n;
+  if (n > static_cast<uint32_t>(LM_CAP)) status |= FL_ROW_LIMIT;
+  // the K-th largest key, then the kept entries (every key at or above it)
+  if (status == 0 && tid < WAVE) {
+    const uint32_t kth = wave_kth_key(static_cast<int>(n), K, sHist, [&](int i) { return static_cast<uint32_t>(c[i] >> 32); });
+    if (lane == 0) s_kth = kth;
+  }
+  __syncthreads();
+  if (status == 0) {
+    const uint32_t kth = s_kth;
+    for (uint32_t i = tid; i < n; i += LM_NT) {
+      if (static_cast<uint32_t>(c[i] >> 32) >= kth) {
+        const uint32_t p = atomicAdd(&s_nk, 1u);
+        if (p < static_cast<uint32_t>(LM_KEEP)) kept[p] = c[i];
+      }
+    }
+  }
+  __syncthreads();
+  const int nk_all = static_cast<int>(s_nk);
+  if (nk_all > LM_KEEP) status |= FL_ROW_LIMIT;
+  const int nk = status == 0 ? nk_all : 0;
+  // sorted descending: value, then ascending vocabulary index
+  if (nk > WAVE) {
+    int np = 128;
+    while (np < nk) np <<= 1;
+    for (int i = nk + tid; i < np; i += LM_NT) kept[i] = 0ull;
+    __syncthreads();
+    lm_sort_desc(kept, np);
+  } else if (tid < WAVE) {
+    const uint64_t v = wave_sort_desc(lane < nk ? kept[lane] : 0ull);
+    kept[lane] = v;
+  }
+  __syncthreads();
+  if (tid >= WAVE) return;
+  if (status == 0 && nk == 0) status |= FL_ROW_ALL_MASKED;
+
+  // ---------------- decisions (wave 0), fl_sample's arithmetic on the sorted kept values
+  const float T = a.temperature[b], TP = a.top_p[b], MP = a.min_p[b];
+  const float U = fminf(fmaxf(a.uniforms[b], 0.0f), 0.99999994f);
+  auto y_of = [&](int j) { return BF16::to_f32(bits_of_asc16(static_cast<uint32_t>(kept[j] >> 32))); };
+  auto idx_of = [&](int j) { return static_cast<int64_t>(~static_cast<uint32_t>(kept[j] & 0xFFFFFFFFull)); };
+  const float M = status == 0 ? y_of(0) : 0.0f;
+  auto E = [&](int j) { return expf(y_of(j) - M); };
+  // fixed-point mass of the first L kept values
+  auto mass = [&](int L) {
+    uint64_t s = 0;
+    for (int j = lane; j < L; j += WAVE) s += to_fx(E(j));
+    return wave_reduce(s, OpAdd());
+  };
+  // first j < L with pred(j) (L if none); pred monotone along j
+  auto first = [&](int L, auto&& pred) {
+    int f = L;
+    for (int j0 = 0; j0 < L && f == L; j0 += WAVE) {
+      const uint64_t m = __ballot(j0 + lane < L && pred(j0 + lane));
+      if (m) f = j0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+    }
+    return f;
+  };
+  int L = nk;
+  int64_t tok = -1;
+  float lp = __builtin_nanf("");
+  if (status == 0) {
+    double S = from_fx(mass(L));
+    if (MP > 0.0f) {  // min-p (sampling.py:40-43)
+      const float r = 1.0f / static_cast<float>(S);
+      const float thr = BF16::rn(BF16::rn(r) * MP);
+      const int Lm = first(L, [&](int j) { return BF16::rn(E(j) * r) < thr; });
+      if (Lm < L) {
+        L = Lm;
+        S = from_fx(mass(L));
+      }
+    }
+    if (TP > 0.0f && TP < 1.0f) {  // top-p (sampling.py:45-51)
+      const float r1 = 1.0f / static_cast<float>(S);
+      const float t = BF16::rn(TP);
+      // position j removed when round(round_f32(C_j) - p_j) >= round(top_p),
+      // C_j the inclusive cumulative of the rounded probabilities (exact fixed point)
+      uint64_t base = 0;
+      int cut = L;
+      for (int j0 = 0; j0 < L && cut == L; j0 += WAVE) {
+        const int j = j0 + lane;
+        const float p = j < L ? BF16::rn(E(j) * r1) : 0.0f;
+        const uint64_t ci = base + wave_incl_scan(static_cast<uint64_t>(to_fx(p)));
+        const bool removed = j < L && BF16::rn(BF16::rn(static_cast<float>(from_fx(ci))) - p) >= t;
+        const uint64_t m = __ballot(removed);
+        if (m) cut = j0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+        base = readlane64(ci, WAVE - 1);
+      }
+      L = cut;
+    }
+    if (L <= 0) {
+      status |= FL_ROW_ALL_MASKED;
+    } else {
+      const double SK = from_fx(mass(L));
+      const float rK = 1.0f / static_cast<float>(SK);
+      int js = 0;
+      if (T <= 0.0f) {
+        // greedy (sampling.py:59-60): first index among the maximal rounded probabilities
+        const float qmax = BF16::rn(E(0) * rK);
+        const int last = first(L, [&](int j) { return BF16::rn(E(j) * rK) != qmax; });
+        int64_t best = 0x7fffffffffffffffll;
+        for (int j = lane; j < last; j += WAVE) best = min(best, idx_of(j));
+        best = wave_reduce(best, OpMin());
+        tok = best;
+        js = 0;
+      } else {
+        // inverse CDF over the kept values in descending order (ties by index)
+        uint64_t Q = 0;
+        for (int j = lane; j < L; j += WAVE) Q += to_fx(BF16::rn(E(j) * rK));
+        Q = wave_reduce(Q, OpAdd());
+        const uint64_t target = __double2ull_rd(static_cast<double>(U) * static_cast<double>(Q));
+        uint64_t base = 0;
+        js = -1;
+        for (int j0 = 0; j0 < L && js < 0; j0 += WAVE) {
+          const int j = j0 + lane;
+          const uint64_t q = j < L ? to_fx(BF16::rn(E(j) * rK)) : 0ull;
+          const uint64_t ci = base + wave_incl_scan(q);
+          const uint64_t m = __ballot(j < L && ci > target);
+          if (m) js = j0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+          base = readlane64(ci, WAVE - 1);
+        }
+        if (js < 0) js = 0;  // (no positive mass: every kept probability rounds to zero)
+        tok = idx_of(js);
+      }
+      // log_softmax(filtered)[tok] as torch evaluates it on a bf16 tensor (sampling.py:97-98)
+      const float ysel = T <= 0.0f ? M : y_of(js);
+      lp = BF16::rn((ysel - M) - BF16::rn(logf(BF16::rn(static_cast<float>(SK)))));
+    }
+  }
+  if (status != 0) {
+    tok = -1;
+    lp = __builtin_nanf("");
+  }
+  if (lane == 0) {
+    a.out_token[b] = tok;
+    a.out_status[b] = static_cast<int32_t>(status);
+    if (a.out_logprob) a.out_logprob[b] = lp;
+  }
+}
+
+// ---------------------------------------------------------------- launch
+size_t lm_head_workspace_bytes(int64_t batch, int64_t vocab) { return lm_ws_bytes(batch, vocab); }
+
+hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s) {
+  const LmWs ws = lm_ws(a.workspace, a.batch, a.vocab);
+  const dim3 rows(static_cast<unsigned>(a.batch));
+  hipLaunchKernelGGL(k_lm_prep, rows, dim3(LM_NT), 0, s, a, ws);
+  const dim3 stiles(static_cast<unsigned>((ws.ns + 63) / 64));
+  const dim3 tiles(static_cast<unsigned>((a.vocab + 255) / 256));
+  const bool sc = a.softcap > 0.0f;
+  const int mb = static_cast<int>((a.batch + 15) / 16);
+  auto run = [&](auto tag_mb, auto tag_sc) {
+    constexpr int MB = decltype(tag_mb)::value;
+    constexpr bool SC = decltype(tag_sc)::value;
+    hipLaunchKernelGGL((k_lm_gemm<MB, SC, true>), stiles, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL(k_lm_thresh, rows, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_gemm<MB, SC, false>), tiles, dim3(LM_NT), 0, s, a, ws);
+  };
+  using T1 = std::integral_constant<int, 1>;
+  using T2 = std::integral_constant<int, 2>;
+  using T4 = std::integral_constant<int, 4>;
+  if (mb <= 1) sc ? run(T1{}, std::true_type{}) : run(T1{}, std::false_type{});
+  else if (mb <= 2) sc ? run(T2{}, std::true_type{}) : run(T2{}, std::false_type{});
+  else sc ? run(T4{}, std::true_type{}) : run(T4{}, std::false_type{});
+  hipLaunchKernelGGL(k_lm_pick, rows, dim3(LM_NT), 0, s, a, ws);
+  return hipGetLastError();
+}
+
+}  // namespace fl

@@ -45,17 +45,22 @@ def _c_layout():
 #include "fl_sampler.h"
 #define F(S, m) printf(#S "." #m " %zu\n", offsetof(S, m));
 int main(void) {
-  printf("fl_row_desc %zu\nfl_sample_args %zu\nfl_spec_args %zu\n", sizeof(fl_row_desc), sizeof(fl_sample_args),
-         sizeof(fl_spec_args));
+  printf("fl_row_desc %zu\nfl_sample_args %zu\nfl_spec_args %zu\nfl_lm_head_args %zu\nfl_row_stats_args %zu\n",
+         sizeof(fl_row_desc), sizeof(fl_sample_args), sizeof(fl_spec_args), sizeof(fl_lm_head_args),
+         sizeof(fl_row_stats_args));
   F(fl_row_desc, y_cut) F(fl_row_desc, idx_cut) F(fl_row_desc, shift) F(fl_row_desc, inv_mass)
   F(fl_row_desc, mass) F(fl_row_desc, status) F(fl_row_desc, n_kept)
   %SAMPLE%
   %SPEC%
+  %LMHEAD%
+  %STATS%
   return 0;
 }
 '''
     src = src.replace("%SAMPLE%", " ".join(f"F(fl_sample_args, {n})" for n, _ in _lib.SampleArgs._fields_))
     src = src.replace("%SPEC%", " ".join(f"F(fl_spec_args, {n})" for n, _ in _lib.SpecArgs._fields_))
+    src = src.replace("%LMHEAD%", " ".join(f"F(fl_lm_head_args, {n})" for n, _ in _lib.LmHeadArgs._fields_))
+    src = src.replace("%STATS%", " ".join(f"F(fl_row_stats_args, {n})" for n, _ in _lib.RowStatsArgs._fields_))
     tmp = os.path.join(os.environ.get("TMPDIR", "/tmp"), f"fl_layout_{os.getpid()}")
     os.makedirs(tmp, exist_ok=True)
     with open(os.path.join(tmp, "layout.c"), "w") as f:
@@ -72,7 +77,10 @@ def test_struct_layout_matches_ctypes():
     assert c["fl_row_desc"] == _lib.ROW_DESC_BYTES
     assert c["fl_sample_args"] == ctypes.sizeof(_lib.SampleArgs)
     assert c["fl_spec_args"] == ctypes.sizeof(_lib.SpecArgs)
-    for S, cls in (("fl_sample_args", _lib.SampleArgs), ("fl_spec_args", _lib.SpecArgs)):
+    assert c["fl_lm_head_args"] == ctypes.sizeof(_lib.LmHeadArgs)
+    assert c["fl_row_stats_args"] == ctypes.sizeof(_lib.RowStatsArgs)
+    for S, cls in (("fl_sample_args", _lib.SampleArgs), ("fl_spec_args", _lib.SpecArgs),
+                   ("fl_lm_head_args", _lib.LmHeadArgs), ("fl_row_stats_args", _lib.RowStatsArgs)):
         for name, _ in cls._fields_:
             assert c[f"{S}.{name}"] == getattr(cls, name).offset, f"{S}.{name}"
 
@@ -237,3 +245,41 @@ def test_row_stats_argument_checks():
     assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_EINVAL
     a.dtype, a.rows = 1, 0                  # nothing to do
     assert L.fl_row_stats(ctypes.byref(a), None) == _lib.FL_OK
+
+
+def test_lm_head_argument_errors():
+    """fl_lm_head_sample's checks, all before anything touches a GPU."""
+    L = _lib.lib()
+    a = _lib.LmHeadArgs()
+    a.struct_size = ctypes.sizeof(_lib.LmHeadArgs)
+    a.dtype = _lib.FL_DTYPE_BF16
+    a.batch, a.dim, a.vocab, a.ld_hidden = 4, 256, 1000, 256
+    for f in ("hidden", "weight", "temperature", "top_k", "top_p", "min_p", "uniforms", "out_token", "out_status"):
+        setattr(a, f, 0x10000)
+    n = ctypes.c_size_t(0)
+    assert L.fl_lm_head_workspace_bytes(4, 1000, ctypes.byref(n)) == _lib.FL_OK
+    # three int32 arrays (256-byte aligned), a 32-word bitmap per row, 4096 candidates per row
+    # (+ the keys of the sampled rows: all 1000 rows at this vocabulary size, 2 bytes each, 256-byte aligned)
+    assert n.value == 3 * 256 + 512 + 8192 + 8 * 4 * 4096
+    assert L.fl_lm_head_workspace_bytes(65, 1000, ctypes.byref(n)) == _lib.FL_EINVAL
+    a.workspace, a.workspace_bytes = 0x100000, n.value
+    cases = [(dict(dtype=_lib.FL_DTYPE_F32), _lib.FL_ENOTSUP, "bf16"),
+             (dict(dim=100, ld_hidden=100), _lib.FL_EINVAL, "multiple of 64"),
+             (dict(batch=65), _lib.FL_ENOTSUP, "limits"),
+             (dict(ld_hidden=128), _lib.FL_EINVAL, "ld_hidden"),
+             (dict(softcap=-1.0), _lib.FL_EINVAL, "softcap"),
+             (dict(top_k=None), _lib.FL_EINVAL, "NULL"),
+             (dict(workspace_bytes=100), _lib.FL_EINVAL, "workspace"),
+             (dict(workspace=0x100010), _lib.FL_EINVAL, "aligned"),
+             (dict(hidden=0x10008), _lib.FL_EINVAL, "16-byte"),
+             (dict(hist_ids=0x20000), _lib.FL_EINVAL, "hist_len"),
+             (dict(struct_size=8), _lib.FL_EINVAL, "struct_size")]
+    for change, code, needle in cases:
+        b = _lib.LmHeadArgs()
+        ctypes.memmove(ctypes.byref(b), ctypes.byref(a), ctypes.sizeof(b))
+        for k, v in change.items():
+            setattr(b, k, v)
+        assert L.fl_lm_head_sample(ctypes.byref(b), None) == code, change
+        assert needle in L.fl_last_error().decode(), (change, L.fl_last_error())
+    a.batch = 0
+    assert L.fl_lm_head_sample(ctypes.byref(a), None) == _lib.FL_OK
