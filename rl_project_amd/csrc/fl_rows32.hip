@@ -567,6 +567,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
   if (X.pen) anchored = tdiv ? read1<true, true>(sh, S, X, V, c, km, nfin, bad) : read1<false, true>(sh, S, X, V, c, km, nfin, bad);
   else anchored = tdiv ? read1<true, false>(sh, S, X, V, c, km, nfin, bad) : read1<false, false>(sh, S, X, V, c, km, nfin, bad);
   if (!anchored) return false;
+  FL_MARK(1);
   const uint32_t kmx = block_reduce<uint32_t>(km, OpMax(), sh.redu);
   const uint32_t bad_all = block_reduce<uint32_t>(bad, OpOr(), sh.redu);
   const uint32_t nf = block_reduce<uint32_t>(nfin, OpAdd(), sh.redu);
@@ -611,6 +612,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     }
   }
   __syncthreads();
+  FL_MARK(2);
   auto Pn = [&](int b) -> uint32_t { return b < NBF ? sh.pc[b] : tc; };
   auto Qm = [&](int b) -> uint64_t { return b < NBF ? sh.acc[b] : tm; };
 
@@ -739,6 +741,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     }
   }
   __syncthreads();
+  FL_MARK(3);
   const int32_t st = sh.fplan[1];
   if (st != 0) {
     o.status = st;
@@ -807,6 +810,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
       }
       __syncthreads();
     }
+    FL_MARK(4);
     // interval ends of the plain (0) and history (1) classes; unused ranges empty
     float xl0[NRANGE], xh0[NRANGE], xl1[NRANGE], xh1[NRANGE];
 #pragma unroll
@@ -835,6 +839,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     if (X.pen) stage(std::true_type{});
     else stage(std::false_type{});
     __syncthreads();
+    FL_MARK(5);
     const int ns = static_cast<int>(sh.ncand);
     if (ns > CAP) return false;
     // staged raw logits -> candidates (key << 32 | ~index); non-members -> 0
@@ -852,6 +857,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     // members first (every member word is nonzero)
     if (ns <= NT) rank_sort_desc(sh.cand, sh.cscan, ns);
     else bitonic_desc(sh.cand, ns);
+    FL_MARK(6);
     const int n = ngath;
 
     // inclusive mass prefix at each candidate
@@ -961,6 +967,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
       }
     }
     __syncthreads();
+    FL_MARK(7);
     if (!sh.fplan[0]) return false;
     o.status = sh.fplan[1];
     tau = sh.fkey[1];
@@ -1001,6 +1008,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
   const bool pen = H > 0;
   const int nch = (V + 3) >> 2;
+  FL_MARK(0);
 
   if (tid == 0) {
     sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
@@ -1513,6 +1521,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
       a.out_desc[b] = dsc;
     }
   }
+  FL_MARK(9);
 }
 
 // ------------------------------------------------------------------ launch
@@ -1523,3 +1532,11 @@ hipError_t launch_sample_rows32(const fl_sample_args& a, hipStream_t s) {
 }
 
 }  // namespace fl
+
+#ifdef FL_PHASE_TIMES
+// Tuning builds only: copy the phase timestamps this kernel recorded.
+extern "C" int fl_debug_phase_ts32(uint64_t* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * (192 + 2048), 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
