@@ -31,10 +31,17 @@ Pinning of each function (what checks it besides retyping):
     sample_rows          composition of the above, per-row loop of
                          ``engine.py:114-139``; stop membership checked on
                          hand-built cases.
+    token_logprob        against the float64 log-softmax of the filtered row
+                         (within the dtype's rounding of the kept mass and its
+                         log, as torch evaluates log_softmax), -log n on rows
+                         of n equal kept values, planted mistakes (the
+                         unfiltered row, a missing shift) fail.
     speculative_verify   accept rule and residual of ``speculative.py:63-75``;
                          pinned by p == q (always accept), disjoint supports
                          (always reject, residual == p), and a chi-square test
                          that emitted tokens follow the target distribution.
+    filtered_probs,      the parts of speculative_verify, pinned with it.
+    residual_token
 """
 
 from __future__ import annotations
