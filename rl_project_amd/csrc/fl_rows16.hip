@@ -359,7 +359,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
   uint4 d[NCH];
 #pragma unroll
   for (int j = 0; j < EARLY_CHUNKS; ++j) {
-    d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+    d[j] = buf_load16_once(rrow, 16u * tid, 16u * NT * j);
     __builtin_amdgcn_sched_barrier(0);
   }
   // ------------------------------------------------ clear LDS
@@ -402,7 +402,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
   // late would hold back the counting of all chunks after it)
 #pragma unroll
   for (int j = EARLY_CHUNKS; j < NCH; ++j) {
-    d[j] = buf_load16(rrow, 16u * tid, 16u * NT * j);
+    d[j] = buf_load16_once(rrow, 16u * tid, 16u * NT * j);
     __builtin_amdgcn_sched_barrier(0);
   }
 
