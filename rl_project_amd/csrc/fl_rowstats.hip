@@ -152,7 +152,7 @@ __global__ __launch_bounds__(NT_RS) void k_row_stats(const fl_row_stats_args a) 
   Acc acc = {-__builtin_inff(), 0.0, 0.0, -__builtin_inff(), 0.0, 0.0};
   auto load = [&](__amdgpu_buffer_rsrc_t rs, int c, float (&x)[N]) __attribute__((always_inline)) {
     if (aligned && c < nfull) {
-      C::unpack(buf_load16(rs, 16u * c, 0u), x);
+      C::unpack(buf_load16_once(rs, 16u * c, 0u), x);  // (read once: 207 -> 201 us at 4096 x 128256 bf16)
     } else {
 #pragma unroll
       for (int e = 0; e < N; ++e) x[e] = N * c + e < V ? C::elem(rs, N * c + e) : -__builtin_inff();
