@@ -4,10 +4,10 @@
 //
 //   prep    one work-group per row: the row's history bitmap (one bit per
 //           vocabulary id, which also de-duplicates the ids) and counters;
-//   sample  the gemm below over every S-th vocabulary row (ns <= 8192 rows,
+//   sample  a gemm over every S-th vocabulary row (ns <= 8192 rows,
 //           S = ceil(vocab / 8192)), in tiles of 64 rows so that many work-groups
 //           share the work; it stores each sampled value's order key.  A
-//           logit's value does not depend on its tile: the same MFMA chain
+//           logit's value does not depend on its kernel: the same MFMA chain
 //           over the same dim order produces it in both gemms;
 //   thresh  one work-group per row: the k-th largest sampled key.  The sampled
 //           values are a subset of the row's, so at least k of the row's values
@@ -15,8 +15,8 @@
 //   gemm    logits = hidden · weightᵀ on the matrix cores
 //           (v_mfma_f32_16x16x32_bf16, fp32 accumulation), one work-group per
 //           256 vocabulary rows and every batch row.  The weight streams from
-//           HBM once, straight into a three-deep register ring; the hidden
-//           states go through LDS two stages ahead.  Epilogue per logit: bf16
+//           HBM once, in whole 128-byte lines, through a double-buffered LDS
+//           stage with the hidden states.  Epilogue per logit: bf16
 //           rounding (the logits tensor the reference would hold), then
 //           soft-cap, penalty and temperature as fl_sample applies them; the
 //           values at or above the row's bound are appended to the row's
@@ -180,45 +180,83 @@ __global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs
   }
 }
 
-// ---------------------------------------------------------------- gemm + epilogue
-// MB: 16-row blocks of the batch (1, 2 or 4).  SC: a soft-cap.  SAMPLE: the
-// sampled rows (16 per wave, 64 per work-group), keys stored; otherwise 64
-// contiguous vocabulary rows per wave, 256 per work-group, candidates
-// appended.  Each 16 x 16 block of logits is one wave's MFMA chain over the
-// dim in the same order in both forms, so a sampled value equals the main
-// gemm's value of the same logit bit for bit.
-template <int MB, bool SC, bool SAMPLE>
-__global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs ws) {
-  constexpr int NB = SAMPLE ? 1 : 4;        // 16-row weight blocks per wave
-  constexpr int TILE = 16 * NB * (LM_NT / WAVE);
+// ---------------------------------------------------------------- gemm epilogue
+// One lane's logits after its MFMA chains: acc[mb][nb][r] is batch row
+// 16 mb + 4 l4 + r and vocabulary row col(nb) (negative: past the end).  Each
+// value is rounded to bf16 (the logit; stored to out_logits by the main gemm),
+// then soft-capped, penalised and divided by the temperature as fl_sample
+// does; put(m, nb, key) receives its order key (0 for NaN and out of range).
+// The main gemm also records NaN and +inf values in the row's status.
+template <int MB, int NB, bool SC, bool MAIN, class Col, class Put>
+__device__ __forceinline__ void lm_epilogue(const fl_lm_head_args& a, const LmWs& ws, const floatx4 (&acc)[MB][NB],
+                                            Col&& col, Put&& put) {
+  const int l4 = (threadIdx.x & (WAVE - 1)) >> 4;
+  const int B = static_cast<int>(a.batch), V = static_cast<int>(a.vocab);
+  const float cap = a.softcap;
+  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+      const bool row_ok = m < B;
+      const int mc = row_ok ? m : 0;
+      const float T = a.temperature[mc];
+      const float RT = T > 0.0f ? 1.0f / T : 0.0f;
+      const bool pen = row_ok && row_penalised(a, mc);
+      const float RP = pen ? a.repetition_penalty[mc] : 1.0f;
+      const uint32_t* hb = ws.bits + static_cast<size_t>(mc) * ws.bw;
+      uint32_t flags = 0;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int n = col(nb);
+        const bool ok = row_ok && n >= 0;
+        const uint32_t xb = BF16::from_f32(acc[mb][nb][r]);
+        if (MAIN && out_logits != nullptr && ok) out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(xb);
+        float z = BF16::to_f32(xb);
+        if constexpr (SC) z = softcap_val<BF16>(z, cap);
+        if (pen && ok && ((hb[n >> 5] >> (n & 31)) & 1u)) z = penalty_val<BF16>(z, RP);
+        const float y = temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
+        const uint32_t yb = BF16::from_f32(y);
+        const bool nan = y != y;
+        flags |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
+        flags |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
+        put(m, nb, (ok && !nan) ? asc16(yb) : 0u);
+      }
+      if (MAIN && flags) atomicOr(&ws.stat[m], flags);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- sample gemm
+// The sampled rows: vocabulary rows e·S for tile entries e, 16 per wave and 64
+// per work-group (ns / 64 work-groups), keys stored to ws.skey.  MB: 16-row
+// blocks of the batch (1, 2 or 4).  SC: a soft-cap.  Each 16 x 16 block of
+// logits is one wave's MFMA chain over the dim in 32-wide steps in ascending
+// order, as in the main gemm below, so a sampled value equals the main gemm's
+// value of the same logit bit for bit.
+template <int MB, bool SC>
+__global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, LmWs ws) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][16 * MB * LM_AST];
-  __shared__ uint16_t sKey[SAMPLE ? 1 : 16 * MB][SAMPLE ? 1 : TILE];
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
-  const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim), V = static_cast<int>(a.vocab);
-  const int S = SAMPLE ? ws.stride : 1;
-  const int nrows = SAMPLE ? ws.ns : V;     // tile entries (sampled rows, or vocabulary rows)
-  const int e0 = blockIdx.x * TILE;
+  const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim);
+  const int S = ws.stride, ns = ws.ns;
+  const int e0 = blockIdx.x * (LM_NT / WAVE) * 16;
   const int l16 = lane & 15, l4 = lane >> 4;
   const uint16_t* W = static_cast<const uint16_t*>(a.weight);
   // hidden rows 0 .. B-1 (rows of the last block past B read zeros)
   const __amdgpu_buffer_rsrc_t rh =
       row_rsrc(a.hidden, 2u * static_cast<uint32_t>(B - 1) * static_cast<uint32_t>(a.ld_hidden) + 2u * D);
 
-  floatx4 acc[MB][NB];
+  floatx4 acc[MB][1];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mb = 0; mb < MB; ++mb) acc[mb][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // lane's weight fragment of block nb, step ks: tile entry 16 NB w + 16 nb +
-  // l16, vocabulary row (e0 + entry)·S (entries past the end read the last
-  // row; their results are dropped), dim k0 + 32 ks + 8 l4 .. +7
-  const uint16_t* wp[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int e = min(e0 + 16 * NB * w + 16 * nb + l16, nrows - 1);
-    wp[nb] = W + static_cast<int64_t>(e) * S * D + 8 * l4;
-  }
+  // lane's weight fragment, step ks: tile entry 16 w + l16, vocabulary row
+  // (e0 + entry)·S (entries past the end read the last row; their results are
+  // dropped), dim k0 + 32 ks + 8 l4 .. +7
+  const int eme = e0 + 16 * w + l16;
+  const uint16_t* wp = W + static_cast<int64_t>(min(eme, ns - 1)) * S * D + 8 * l4;
   // hidden-state stage: 16 MB rows x 64 columns = 128 MB pieces of 16 bytes
   constexpr int APIECES = (16 * MB * LM_KC / 8 + LM_NT - 1) / LM_NT;
   auto load_a = [&](uint4 (&ap)[APIECES], int k0) {
@@ -239,22 +277,17 @@ __global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs
       if (row < 16 * MB) *reinterpret_cast<uint4*>(&sA[st][row * LM_AST + 8 * seg]) = ap[s];
     }
   };
-  auto load_w = [&](uint4 (&wf)[2][NB], int k0) {
+  auto load_w = [&](uint4 (&wf)[2], int k0) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) wf[ks][nb] = *reinterpret_cast<const uint4*>(wp[nb] + k0 + 32 * ks);
+    for (int ks = 0; ks < 2; ++ks) wf[ks] = *reinterpret_cast<const uint4*>(wp + k0 + 32 * ks);
   };
-  auto mfma_stage = [&](int st, const uint4 (&wf)[2][NB]) {
+  auto mfma_stage = [&](int st, const uint4 (&wf)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const bf16x8 af = *reinterpret_cast<const bf16x8*>(&sA[st][(16 * mb + l16) * LM_AST + 32 * ks + 8 * l4]);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8, wf[ks][nb]),
-                                                                acc[mb][nb], 0, 0, 0);
+        acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8, wf[ks]), acc[mb][0], 0, 0, 0);
       }
     }
   };
@@ -264,7 +297,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs
   // its weight slot with stage it + LM_NST.
   const int NIT = D / LM_KC;
   uint4 an[APIECES];
-  uint4 wr[LM_NST][2][NB];
+  uint4 wr[LM_NST][2];
   load_a(an, 0);
 #pragma unroll
   for (int u = 0; u < LM_NST; ++u)
@@ -285,84 +318,154 @@ __global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs
       }
     }
   }
+  lm_epilogue<MB, 1, SC, false>(
+      a, ws, acc, [&](int) { return eme < ns ? eme * S : -1; },
+      [&](int m, int, uint32_t key) {
+        if (m < B && eme < ns) ws.skey[static_cast<size_t>(m) * ns + eme] = static_cast<uint16_t>(key);
+      });
+}
 
-  // ---------------- epilogue: values and their keys
-  // lane holds (m, tile entry c) = (16 mb + 4 l4 + r, 16 NB w + 16 nb + l16) in
-  // acc[mb][nb][r]; its vocabulary row is (e0 + c)·S
-  const float cap = a.softcap;
-  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+// ---------------------------------------------------------------- main gemm
+// logits = hidden · weightᵀ for 256 contiguous vocabulary rows (64 per wave)
+// and every batch row, then the epilogue and the candidates at or above each
+// row's bound.  A stage is 64 dims of the 256 weight rows and the 16 MB
+// hidden rows, staged through LDS twice buffered: each thread loads 16-byte
+// pieces (eight lanes cover one 128-byte line of a weight row; the weight
+// with the non-temporal policy, read once), stores them to the other buffer
+// one iteration later, and the waves read their MFMA fragments from LDS.
+// LDS holds 16-byte granule g of row r at r·8 + (g xor ((r >> 1) & 7)): the
+// fragment reads (16 rows, one granule column) and the stores (8 granules of
+// one row) then spread over all banks.
+template <int MB, bool SC>
+__global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs ws) {
+  constexpr int NB = 4;                           // 16-row weight blocks per wave
+  constexpr int TILE = LM_NTILE;
+  constexpr int MR = 16 * MB;                     // batch rows of the tile
+  constexpr int STAGE_Q = (TILE + MR) * 8;        // 16-byte granules per stage
+  constexpr int KEY_Q = (MR * TILE * 2 + 15) / 16;
+  constexpr int SMEM_Q = (2 * STAGE_Q > KEY_Q) ? 2 * STAGE_Q : KEY_Q;
+  static_assert(TILE == 16 * NB * (LM_NT / WAVE) && LM_KC == 64, "stage shape");
+  __shared__ __attribute__((aligned(16))) uint4 smem[SMEM_Q];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
+  const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim), V = static_cast<int>(a.vocab);
+  const int e0 = blockIdx.x * TILE;
+  const int l16 = lane & 15, l4 = lane >> 4;
+  const uint16_t* W = static_cast<const uint16_t*>(a.weight);
+  const __amdgpu_buffer_rsrc_t rh =
+      row_rsrc(a.hidden, 2u * static_cast<uint32_t>(B - 1) * static_cast<uint32_t>(a.ld_hidden) + 2u * D);
+  // the tile's weight rows (rows past the vocabulary read zeros)
+  const __amdgpu_buffer_rsrc_t rw = row_rsrc(W + static_cast<int64_t>(e0) * D,
+                                             2u * static_cast<uint32_t>(min(TILE, V - e0)) * static_cast<uint32_t>(D));
+  auto gran = [](int r, int g) { return r * 8 + (g ^ ((r >> 1) & 7)); };
+
+  floatx4 acc[MB][NB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * mb + 4 * l4 + r;
-      const bool row_ok = m < B;
-      const int mc = row_ok ? m : 0;
-      const float T = a.temperature[mc];
-      const float RT = T > 0.0f ? 1.0f / T : 0.0f;
-      const bool pen = row_ok && row_penalised(a, mc);
-      const float RP = pen ? a.repetition_penalty[mc] : 1.0f;
-      const uint32_t* hb = ws.bits + static_cast<size_t>(mc) * ws.bw;
-      uint32_t flags = 0;
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // thread t loads weight rows (t >> 3) + 32 p, granule t & 7, and hidden
+  // pieces t + 256 p (row >> 3, granule & 7)
+  constexpr int WP = TILE * 8 / LM_NT;             // 8
+  constexpr int AP = (MR * 8 + LM_NT - 1) / LM_NT;  // 1 or 2
+  uint4 wreg[WP], areg[AP];
+  auto load_stage = [&](int k0) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int c = 16 * NB * w + 16 * nb + l16;
-        const int e = e0 + c;
-        const int n = e * S;
-        const bool ok = row_ok && e < nrows;
-        const uint32_t xb = BF16::from_f32(acc[mb][nb][r]);
-        if (!SAMPLE && out_logits != nullptr && ok) out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(xb);
-        float z = BF16::to_f32(xb);
-        if constexpr (SC) z = softcap_val<BF16>(z, cap);
-        if (pen && ok && ((hb[n >> 5] >> (n & 31)) & 1u)) z = penalty_val<BF16>(z, RP);
-        const float y = temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
-        const uint32_t yb = BF16::from_f32(y);
-        const bool nan = y != y;
-        const uint32_t key = (ok && !nan) ? asc16(yb) : 0u;
-        if constexpr (SAMPLE) {
-          if (ok) ws.skey[static_cast<size_t>(m) * ws.ns + e] = static_cast<uint16_t>(key);
-        } else {
-          flags |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
-          flags |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
-          sKey[m][c] = static_cast<uint16_t>(key);
-        }
-      }
-      if (!SAMPLE && flags) atomicOr(&ws.stat[m], flags);
+    for (int p = 0; p < WP; ++p) {
+      const int r = (tid >> 3) + 32 * p, g = tid & 7;
+      wreg[p] = buf_load16_once(rw, 2u * (static_cast<uint32_t>(r) * D + k0 + 8 * g), 0u);
     }
-  }
-  if constexpr (!SAMPLE) {
+#pragma unroll
+    for (int p = 0; p < AP; ++p) {
+      const int idx = tid + LM_NT * p;
+      const int r = idx >> 3, g = idx & 7;
+      areg[p] = (r < MR && r < B)
+                    ? buf_load16(rh, 2u * (static_cast<uint32_t>(r) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * g), 0u)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_stage = [&](int st) {
+    uint4* s = smem + st * STAGE_Q;
+#pragma unroll
+    for (int p = 0; p < WP; ++p) s[gran((tid >> 3) + 32 * p, tid & 7)] = wreg[p];
+#pragma unroll
+    for (int p = 0; p < AP; ++p) {
+      const int idx = tid + LM_NT * p;
+      if ((idx >> 3) < MR) s[gran(TILE + (idx >> 3), idx & 7)] = areg[p];
+    }
+  };
+
+  // Pipeline: iteration `it` multiplies stage it from LDS, stores stage it + 1
+  // (loaded during it - 1) into the other buffer and loads stage it + 2.
+  const int NIT = D / LM_KC;
+  load_stage(0);
+  store_stage(0);
+  if (NIT > 1) load_stage(LM_KC);
+  __syncthreads();
+  for (int it = 0; it < NIT; ++it) {
+    const int st = it & 1;
+    const uint4* s = smem + st * STAGE_Q;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 bfr[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        bfr[nb] = __builtin_bit_cast(bf16x8, s[gran(64 * w + 16 * nb + l16, 4 * ks + l4)]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bf16x8 af = __builtin_bit_cast(bf16x8, s[gran(TILE + 16 * mb + l16, 4 * ks + l4)]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[nb], acc[mb][nb], 0, 0, 0);
+      }
+    }
+    if (it + 1 < NIT) {
+      store_stage(st ^ 1);
+      if (it + 2 < NIT) load_stage((it + 2) * LM_KC);
+    }
     __syncthreads();
-    // ---------------- per row: append the tile's values at or above the bound
-    const int rows = min(B, 16 * MB);
-    for (int m = w; m < rows; m += LM_NT / WAVE) {
-      const int K = a.top_k[m];
-      if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) continue;
-      const uint32_t thr = ws.thr[m];
-      uint64_t sel[4];
-      uint32_t k4[4];
-      int total = 0;
+  }
+
+  // ---------------- epilogue: keys of the tile (LDS reused), then per row the
+  // tile's keys at or above the bound appended to the row's candidates
+  uint16_t (*sKey)[TILE] = reinterpret_cast<uint16_t (*)[TILE]>(smem);
+  lm_epilogue<MB, NB, SC, true>(
+      a, ws, acc,
+      [&](int nb) {
+        const int n = e0 + 64 * w + 16 * nb + l16;
+        return n < V ? n : -1;
+      },
+      [&](int m, int nb, uint32_t key) { sKey[m][64 * w + 16 * nb + l16] = static_cast<uint16_t>(key); });
+  __syncthreads();
+  const int rows = min(B, MR);
+  for (int m = w; m < rows; m += LM_NT / WAVE) {
+    const int K = a.top_k[m];
+    if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) continue;
+    const uint32_t thr = ws.thr[m];
+    uint64_t sel[4];
+    uint32_t k4[4];
+    int total = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        k4[q] = sKey[m][lane + WAVE * q];
-        sel[q] = __ballot(k4[q] != 0u && k4[q] >= thr);
-        total += __popcll(sel[q]);
-      }
-      if (total == 0) continue;
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&ws.cnt[m], static_cast<uint32_t>(total));
-      base = static_cast<uint32_t>(__shfl(static_cast<int>(base), 0, WAVE));
-      uint64_t* cand = ws.cand + static_cast<size_t>(m) * LM_CAP;
-      const uint64_t below = (1ull << lane) - 1ull;
-      uint32_t pos = base;
+    for (int q = 0; q < 4; ++q) {
+      k4[q] = sKey[m][lane + WAVE * q];
+      sel[q] = __ballot(k4[q] != 0u && k4[q] >= thr);
+      total += __popcll(sel[q]);
+    }
+    if (total == 0) continue;
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&ws.cnt[m], static_cast<uint32_t>(total));
+    base = static_cast<uint32_t>(__shfl(static_cast<int>(base), 0, WAVE));
+    uint64_t* cand = ws.cand + static_cast<size_t>(m) * LM_CAP;
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t pos = base;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if ((sel[q] >> lane) & 1ull) {
-          const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel[q] & below));
-          const uint32_t n = static_cast<uint32_t>(e0 + lane + WAVE * q);
-          if (p < static_cast<uint32_t>(LM_CAP)) cand[p] = (static_cast<uint64_t>(k4[q]) << 32) | static_cast<uint32_t>(~n);
-        }
-        pos += static_cast<uint32_t>(__popcll(sel[q]));
+    for (int q = 0; q < 4; ++q) {
+      if ((sel[q] >> lane) & 1ull) {
+        const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel[q] & below));
+        const uint32_t n = static_cast<uint32_t>(e0 + lane + WAVE * q);
+        if (p < static_cast<uint32_t>(LM_CAP)) cand[p] = (static_cast<uint64_t>(k4[q]) << 32) | static_cast<uint32_t>(~n);
       }
+      pos += static_cast<uint32_t>(__popcll(sel[q]));
     }
   }
 }
@@ -596,9 +699,9 @@ hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s) {
   auto run = [&](auto tag_mb, auto tag_sc) {
     constexpr int MB = decltype(tag_mb)::value;
     constexpr bool SC = decltype(tag_sc)::value;
-    hipLaunchKernelGGL((k_lm_gemm<MB, SC, true>), stiles, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_sample<MB, SC>), stiles, dim3(LM_NT), 0, s, a, ws);
     hipLaunchKernelGGL(k_lm_thresh, rows, dim3(LM_NT), 0, s, a, ws);
-    hipLaunchKernelGGL((k_lm_gemm<MB, SC, false>), tiles, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_gemm<MB, SC>), tiles, dim3(LM_NT), 0, s, a, ws);
   };
   using T1 = std::integral_constant<int, 1>;
   using T2 = std::integral_constant<int, 2>;
