@@ -40,12 +40,23 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int LM_NT = 256;                 // threads of the gemm and pick work-groups
-constexpr int LM_NTILE = 256;              // vocabulary rows per gemm tile (64 per wave)
+constexpr int LM_NTILE = 256;              // vocabulary rows per gemm tile
+#ifndef LM_GW
+#define LM_GW 8
+#endif
+#ifndef LM_GSLOTS
+#define LM_GSLOTS 2
+#endif
 constexpr int LM_KC = 64;                  // dim per pipeline stage (two MFMA steps of 32)
 constexpr int LM_AST = LM_KC + 8;          // LDS row stride of a hidden-state stage, bf16 elements
-constexpr int LM_NST = 3;                  // weight stages in flight per wave
+constexpr int LM_NST = 8;                  // weight stages in flight per wave of the sample gemm
 constexpr int LM_NSAMPLE = 8192;           // sampled vocabulary rows (at most)
 constexpr int LM_CAP = FL_LM_HEAD_MAX_CAND;
+// Every gemm tile adds its candidate count to each row's counter at the end
+// of the kernel; one counter per 256 bytes spreads those atomics over
+// channels (64 counters in two cache lines cost ~30 us of serialised atomics
+// at 501 tiles x 64 rows).
+constexpr int LM_CNT_LD = 64;
 
 // Ascending order key of a 16-bit float pattern: larger value, larger key;
 // 0 only for the all-ones NaN pattern (the epilogue maps every NaN to 0).
@@ -54,14 +65,16 @@ __device__ __forceinline__ uint32_t bits_of_asc16(uint32_t k) { return bits_of_o
 
 struct LmWs {
   uint32_t* thr;    // [batch] the row's bound (asc16 key; 0: none)
-  uint32_t* cnt;    // [batch] candidates appended
+  uint32_t* cnt;    // [batch, LM_CNT_LD] candidates appended (word 0 of a row's 256 bytes)
   uint32_t* stat;   // [batch] FL_ROW_* bits found by prep and gemm
   uint32_t* bits;   // [batch, bw] history bitmap
-  uint16_t* skey;   // [batch, ns] keys of the sampled rows (entry e: vocabulary row e·S)
+  uint16_t* skey;   // [batch, nsl] keys of the sampled rows (entry e: vocabulary row e·S)
   uint64_t* cand;   // [batch, LM_CAP] (key << 32) | ~vocabulary index
-  int bw;
+  int bw;           // words per bitmap row, a multiple of 4
   int stride;       // S
   int ns;
+  int nsl;          // ns rounded up to a multiple of 8
+  int prep;         // the call passes a penalty: the prep kernel runs and sets stat
 };
 
 __host__ __device__ inline int lm_stride(int64_t vocab) {  // ceil(vocab / 8192): ns <= 8192
@@ -71,29 +84,33 @@ __host__ __device__ inline int lm_ns(int64_t vocab) {
   return static_cast<int>((vocab + lm_stride(vocab) - 1) / lm_stride(vocab));
 }
 __host__ __device__ inline size_t lm_align(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+__host__ __device__ inline int lm_bw(int64_t vocab) { return static_cast<int>(((vocab + 31) / 32 + 3) & ~3); }
+__host__ __device__ inline int lm_nsl(int64_t vocab) { return (lm_ns(vocab) + 7) & ~7; }
 __host__ __device__ inline size_t lm_ws_bytes(int64_t batch, int64_t vocab) {
-  const size_t B = static_cast<size_t>(batch), bw = static_cast<size_t>((vocab + 31) / 32);
-  return 3 * lm_align(4 * B) + lm_align(4 * B * bw) + lm_align(2 * B * static_cast<size_t>(lm_ns(vocab))) +
-         8 * B * LM_CAP;
+  const size_t B = static_cast<size_t>(batch), bw = static_cast<size_t>(lm_bw(vocab));
+  return 2 * lm_align(4 * B) + 4 * B * LM_CNT_LD + lm_align(4 * B * bw) +
+         lm_align(2 * B * static_cast<size_t>(lm_nsl(vocab))) + 8 * B * LM_CAP;
 }
 inline LmWs lm_ws(void* p, int64_t batch, int64_t vocab) {
   const size_t B = static_cast<size_t>(batch);
   char* q = static_cast<char*>(p);
   LmWs w;
-  w.bw = static_cast<int>((vocab + 31) / 32);
+  w.bw = lm_bw(vocab);
   w.stride = lm_stride(vocab);
   w.ns = lm_ns(vocab);
+  w.nsl = lm_nsl(vocab);
+  w.prep = 0;
   size_t off = 0;
   w.thr = reinterpret_cast<uint32_t*>(q + off);
   off += lm_align(4 * B);
   w.cnt = reinterpret_cast<uint32_t*>(q + off);
-  off += lm_align(4 * B);
+  off += 4 * B * LM_CNT_LD;
   w.stat = reinterpret_cast<uint32_t*>(q + off);
   off += lm_align(4 * B);
   w.bits = reinterpret_cast<uint32_t*>(q + off);
   off += lm_align(4 * B * w.bw);
   w.skey = reinterpret_cast<uint16_t*>(q + off);
-  off += lm_align(2 * B * static_cast<size_t>(w.ns));
+  off += lm_align(2 * B * static_cast<size_t>(w.nsl));
   w.cand = reinterpret_cast<uint64_t*>(q + off);
   return w;
 }
@@ -101,6 +118,27 @@ inline LmWs lm_ws(void* p, int64_t batch, int64_t vocab) {
 __device__ __forceinline__ bool row_penalised(const fl_lm_head_args& a, int b) {
   return a.repetition_penalty != nullptr && a.hist_ids != nullptr && a.hist_len != nullptr &&
          a.repetition_penalty[b] != 1.0f;
+}
+
+// Of 256 bin counts, lane holding bins 255 - 4 lane - q in c4[q]: the bin
+// where the count from the top reaches k (-1 when the bins hold fewer than k
+// keys), and in `above` the count of the bins above it.  Called by a whole wave.
+__device__ int wave_top_bin(const uint32_t (&c4)[4], int k, uint32_t& above) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const uint32_t s = c4[0] + c4[1] + c4[2] + c4[3];
+  const uint32_t incl = wave_incl_scan(s);
+  int bin = -1;
+  uint32_t run = incl - s;   // keys in higher bins
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (bin < 0 && run + c4[q] >= static_cast<uint32_t>(k)) bin = 255 - 4 * lane - q;
+    if (bin < 0) run += c4[q];
+  }
+  const uint64_t m = __ballot(bin >= 0);
+  if (m == 0) return -1;
+  const int src = __ffsll(static_cast<unsigned long long>(m)) - 1;
+  above = static_cast<uint32_t>(__shfl(static_cast<int>(run), src, WAVE));
+  return __shfl(bin, src, WAVE);
 }
 
 // The k-th largest of n 16-bit keys (0 when n < k), by one wave: two passes of a 256-bin histogram (high byte, then the
@@ -119,31 +157,14 @@ __device__ uint32_t wave_kth_key(int n, int k, uint32_t* hist, KeyAt&& key_at) {
       else if ((key >> 8) == prefix) atomicAdd(&hist[key & 0xFFu], 1u);
     }
     __builtin_amdgcn_wave_barrier();
-    // bins from the top: lane holds bins 255 - 4 lane .. 252 - 4 lane
-    uint32_t c4[4], s = 0;
+    uint32_t c4[4], above = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = hist[255 - 4 * lane - q];
-      s += c4[q];
-    }
-    const uint32_t incl = wave_incl_scan(s);
-    const uint32_t before = incl - s;   // keys in higher bins
-    // the bin where the count from the top reaches k
-    int bin = -1;
-    uint32_t run = before;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (bin < 0 && run + c4[q] >= static_cast<uint32_t>(k)) bin = 255 - 4 * lane - q;
-      if (bin < 0) run += c4[q];
-    }
-    const uint64_t m = __ballot(bin >= 0);
-    if (m == 0) return 0u;   // fewer than k keys
-    const int src = __ffsll(static_cast<unsigned long long>(m)) - 1;
-    const uint32_t chosen = static_cast<uint32_t>(__shfl(bin, src, WAVE));
-    const uint32_t above = static_cast<uint32_t>(__shfl(static_cast<int>(run), src, WAVE));
+    for (int q = 0; q < 4; ++q) c4[q] = hist[255 - 4 * lane - q];
+    const int bin = wave_top_bin(c4, k, above);
+    if (bin < 0) return 0u;   // fewer than k keys
     k -= static_cast<int>(above);
-    if (pass == 0) prefix = chosen;
-    else return (prefix << 8) | chosen;
+    if (pass == 0) prefix = static_cast<uint32_t>(bin);
+    else return (prefix << 8) | static_cast<uint32_t>(bin);
     __builtin_amdgcn_wave_barrier();
   }
   return 0u;
@@ -152,32 +173,38 @@ __device__ uint32_t wave_kth_key(int n, int k, uint32_t* hist, KeyAt&& key_at) {
 }  // namespace
 
 // ---------------------------------------------------------------- prep
+// Launched when the call passes a penalty and histories; one work-group per
+// row.  A penalised row gets its history bitmap (one bit per vocabulary id,
+// which also de-duplicates the ids); every row gets its status from its
+// history (too long, ids out of range).
 __global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs ws) {
+  __shared__ uint32_t s_flags;
   const int b = blockIdx.x, tid = threadIdx.x;
   uint32_t* bits = ws.bits + static_cast<size_t>(b) * ws.bw;
-  for (int i = tid; i < ws.bw; i += LM_NT) bits[i] = 0u;
-  if (tid == 0) {
-    ws.thr[b] = 0u;
-    ws.cnt[b] = 0u;
-    ws.stat[b] = 0u;
+  const bool pen = row_penalised(a, b);
+  if (tid == 0) s_flags = 0u;
+  if (pen) {
+    uint4* b4 = reinterpret_cast<uint4*>(bits);
+    for (int i = tid; i < ws.bw / 4; i += LM_NT) b4[i] = make_uint4(0u, 0u, 0u, 0u);
   }
   __syncthreads();  // (the bitmap's zeros reach memory before the atomics below)
-  if (!row_penalised(a, b)) return;
-  int H = a.hist_len[b];
+  int H = pen ? a.hist_len[b] : 0;
   if (H > FL_MAX_HISTORY) {
-    if (tid == 0) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_LIMIT));
-    return;
+    if (tid == 0) s_flags = static_cast<uint32_t>(FL_ROW_LIMIT);
+    H = 0;
   }
   if (a.hist_ld > 0 && H > a.hist_ld) {  // (a length past its row: the row's ids only)
-    if (tid == 0) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
+    if (tid == 0) atomicOr(&s_flags, static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
     H = static_cast<int>(a.hist_ld);
   }
   const int32_t* hid = a.hist_ids + static_cast<int64_t>(b) * a.hist_ld;
   for (int i = tid; i < H; i += LM_NT) {
     const int id = hid[i];
-    if (id < 0 || id >= a.vocab) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
+    if (id < 0 || id >= a.vocab) atomicOr(&s_flags, static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
     else atomicOr(&bits[id >> 5], 1u << (id & 31));
   }
+  __syncthreads();
+  if (tid == 0) ws.stat[b] = s_flags;
 }
 
 // ---------------------------------------------------------------- gemm epilogue
@@ -187,13 +214,17 @@ __global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs
 // then soft-capped, penalised and divided by the temperature as fl_sample
 // does; put(m, nb, key) receives its order key (0 for NaN and out of range).
 // The main gemm also records NaN and +inf values in the row's status.
+// Two phases: first every key, with loads only (the rows' parameters and
+// history bits), then every store.  Global stores among the loads would keep
+// the compiler from issuing a later row's loads before an earlier row's
+// stores, one memory round trip per row.
 template <int MB, int NB, bool SC, bool MAIN, class Col, class Put>
 __device__ __forceinline__ void lm_epilogue(const fl_lm_head_args& a, const LmWs& ws, const floatx4 (&acc)[MB][NB],
                                             Col&& col, Put&& put) {
   const int l4 = (threadIdx.x & (WAVE - 1)) >> 4;
   const int B = static_cast<int>(a.batch), V = static_cast<int>(a.vocab);
   const float cap = a.softcap;
-  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+  uint32_t key[MB][4][NB], flags[MB][4];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
@@ -206,24 +237,38 @@ __device__ __forceinline__ void lm_epilogue(const fl_lm_head_args& a, const LmWs
       const bool pen = row_ok && row_penalised(a, mc);
       const float RP = pen ? a.repetition_penalty[mc] : 1.0f;
       const uint32_t* hb = ws.bits + static_cast<size_t>(mc) * ws.bw;
-      uint32_t flags = 0;
+      uint32_t f = 0;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int n = col(nb);
         const bool ok = row_ok && n >= 0;
-        const uint32_t xb = BF16::from_f32(acc[mb][nb][r]);
-        if (MAIN && out_logits != nullptr && ok) out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(xb);
-        float z = BF16::to_f32(xb);
+        float z = BF16::to_f32(BF16::from_f32(acc[mb][nb][r]));
         if constexpr (SC) z = softcap_val<BF16>(z, cap);
         if (pen && ok && ((hb[n >> 5] >> (n & 31)) & 1u)) z = penalty_val<BF16>(z, RP);
         const float y = temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
         const uint32_t yb = BF16::from_f32(y);
         const bool nan = y != y;
-        flags |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
-        flags |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
-        put(m, nb, (ok && !nan) ? asc16(yb) : 0u);
+        f |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
+        f |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
+        key[mb][r][nb] = (ok && !nan) ? asc16(yb) : 0u;
       }
-      if (MAIN && flags) atomicOr(&ws.stat[m], flags);
+      flags[mb][r] = f;
+    }
+  }
+  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        put(m, nb, key[mb][r][nb]);
+        const int n = col(nb);
+        if (MAIN && out_logits != nullptr && m < B && n >= 0)
+          out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(BF16::from_f32(acc[mb][nb][r]));
+      }
+      if (MAIN && flags[mb][r]) atomicOr(&ws.stat[m], flags[mb][r]);
     }
   }
 }
@@ -258,15 +303,14 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
   const int eme = e0 + 16 * w + l16;
   const uint16_t* wp = W + static_cast<int64_t>(min(eme, ns - 1)) * S * D + 8 * l4;
   // hidden-state stage: 16 MB rows x 64 columns = 128 MB pieces of 16 bytes
+  // (pieces of rows past the batch lie past the buffer's range and read zeros)
   constexpr int APIECES = (16 * MB * LM_KC / 8 + LM_NT - 1) / LM_NT;
   auto load_a = [&](uint4 (&ap)[APIECES], int k0) {
 #pragma unroll
     for (int s = 0; s < APIECES; ++s) {
       const int idx = tid + LM_NT * s;
       const int row = idx >> 3, seg = idx & 7;
-      const bool in = row < 16 * MB && row < B;
-      ap[s] = in ? buf_load16(rh, 2u * (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * seg), 0u)
-                 : make_uint4(0, 0, 0, 0);
+      ap[s] = buf_load16(rh, 2u * (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * seg), 0u);
     }
   };
   auto store_a = [&](const uint4 (&ap)[APIECES], int st) {
@@ -292,36 +336,41 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
     }
   };
 
-  // Pipeline: iteration `it` stores the hidden stage it + 1 (loaded during
-  // it - 1) into LDS, loads stage it + 2, multiplies stage it, then refills
-  // its weight slot with stage it + LM_NST.
+  // Pipeline: stage s (its weight fragments and its hidden pieces) lives in
+  // register slot s % LM_NST.  Iteration `it` stores the hidden pieces of
+  // stage it + 1 into LDS buffer (it + 1) & 1, multiplies stage it, and refills
+  // its slot with stage it + LM_NST, so LM_NST - 1 stages stream from memory
+  // during each iteration.  Every load is issued unconditionally, in stage
+  // order (past the last stage, the last stage again, never used), and the
+  // iterations run in whole groups of LM_NST (those past the last stage only
+  // load), so the waits before the LDS stores and the MFMAs leave the later
+  // stages in flight.
   const int NIT = D / LM_KC;
-  uint4 an[APIECES];
-  uint4 wr[LM_NST][2];
-  load_a(an, 0);
+  const int NPAD = (NIT + LM_NST - 1) / LM_NST * LM_NST;
+  auto kc = [&](int st) { return min(st, NIT - 1) * LM_KC; };
+  uint4 wr[LM_NST][2], ar[LM_NST][APIECES];
 #pragma unroll
-  for (int u = 0; u < LM_NST; ++u)
-    if (u < NIT) load_w(wr[u], u * LM_KC);
-  store_a(an, 0);
-  if (NIT > 1) load_a(an, LM_KC);
+  for (int u = 0; u < LM_NST; ++u) {
+    load_w(wr[u], kc(u));
+    load_a(ar[u], kc(u));
+  }
+  store_a(ar[0], 0);
   __syncthreads();
-  for (int it0 = 0; it0 < NIT; it0 += LM_NST) {
+  for (int it0 = 0; it0 < NPAD; it0 += LM_NST) {
 #pragma unroll
     for (int u = 0; u < LM_NST; ++u) {
       const int it = it0 + u;
-      if (it < NIT) {
-        if (it + 1 < NIT) store_a(an, (it + 1) & 1);
-        if (it + 2 < NIT) load_a(an, (it + 2) * LM_KC);
-        mfma_stage(it & 1, wr[u]);
-        if (it + LM_NST < NIT) load_w(wr[u], (it + LM_NST) * LM_KC);
-        __syncthreads();
-      }
+      if (it + 1 < NIT) store_a(ar[(u + 1) % LM_NST], (it + 1) & 1);
+      if (it < NIT) mfma_stage(it & 1, wr[u]);
+      load_w(wr[u], kc(it + LM_NST));
+      load_a(ar[u], kc(it + LM_NST));
+      __syncthreads();
     }
   }
   lm_epilogue<MB, 1, SC, false>(
       a, ws, acc, [&](int) { return eme < ns ? eme * S : -1; },
       [&](int m, int, uint32_t key) {
-        if (m < B && eme < ns) ws.skey[static_cast<size_t>(m) * ns + eme] = static_cast<uint16_t>(key);
+        if (m < B && eme < ns) ws.skey[static_cast<size_t>(m) * ws.nsl + eme] = static_cast<uint16_t>(key);
       });
 }
 
@@ -336,15 +385,18 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
 // LDS holds 16-byte granule g of row r at r·8 + (g xor ((r >> 1) & 7)): the
 // fragment reads (16 rows, one granule column) and the stores (8 granules of
 // one row) then spread over all banks.
-template <int MB, bool SC>
-__global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs ws) {
-  constexpr int NB = 4;                           // 16-row weight blocks per wave
+template <int MB, bool SC, int NW>
+__global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 2))) void k_lm_gemm(const fl_lm_head_args a,
+                                                                                                   LmWs ws) {
+  constexpr int NT = NW * WAVE;
   constexpr int TILE = LM_NTILE;
+  constexpr int RW = TILE / NW;                   // weight rows per wave
+  constexpr int NB = RW / 16;                     // 16-row weight blocks per wave
   constexpr int MR = 16 * MB;                     // batch rows of the tile
   constexpr int STAGE_Q = (TILE + MR) * 8;        // 16-byte granules per stage
   constexpr int KEY_Q = (MR * TILE * 2 + 15) / 16;
   constexpr int SMEM_Q = (2 * STAGE_Q > KEY_Q) ? 2 * STAGE_Q : KEY_Q;
-  static_assert(TILE == 16 * NB * (LM_NT / WAVE) && LM_KC == 64, "stage shape");
+  static_assert(TILE == 16 * NB * NW && LM_KC == 64 && TILE * 8 % NT == 0, "stage shape");
   __shared__ __attribute__((aligned(16))) uint4 smem[SMEM_Q];
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
   const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim), V = static_cast<int>(a.vocab);
@@ -364,66 +416,98 @@ __global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // thread t loads weight rows (t >> 3) + 32 p, granule t & 7, and hidden
-  // pieces t + 256 p (row >> 3, granule & 7)
-  constexpr int WP = TILE * 8 / LM_NT;             // 8
-  constexpr int AP = (MR * 8 + LM_NT - 1) / LM_NT;  // 1 or 2
-  uint4 wreg[WP], areg[AP];
-  auto load_stage = [&](int k0) {
+  // Thread t loads weight rows (t >> 3) + (NT / 8) p, granule t & 7, and
+  // hidden pieces t + NT p (row >> 3, granule & 7), into register slot j; the
+  // stage's dim k0 goes in the SGPR offset.  Rows past the vocabulary (past
+  // the batch) lie past their buffer's range and read zeros: their offset
+  // register alone passes the range.
+  constexpr int WP = TILE * 8 / NT;
+  constexpr int AP = (MR * 8 + NT - 1) / NT;
+  uint32_t vw[WP];
 #pragma unroll
-    for (int p = 0; p < WP; ++p) {
-      const int r = (tid >> 3) + 32 * p, g = tid & 7;
-      wreg[p] = buf_load16_once(rw, 2u * (static_cast<uint32_t>(r) * D + k0 + 8 * g), 0u);
-    }
+  for (int p = 0; p < WP; ++p)
+    vw[p] = 2u * (static_cast<uint32_t>((tid >> 3) + (NT / 8) * p) * D + 8 * (tid & 7));
+  uint32_t va[AP];
+#pragma unroll
+  for (int p = 0; p < AP; ++p) {
+    const int idx = tid + NT * p;
+    va[p] = 2u * (static_cast<uint32_t>(idx >> 3) * static_cast<uint32_t>(a.ld_hidden) + 8 * (idx & 7));
+  }
+  constexpr int NSL = LM_GSLOTS;                   // register slots (stages in flight)
+  constexpr int U = NSL % 2 == 0 ? NSL : 2 * NSL;  // iterations per unrolled group
+  uint4 wreg[NSL][WP], areg[NSL][AP];
+  auto load_stage = [&](int j, int k0) {
+#pragma unroll
+    for (int p = 0; p < WP; ++p) wreg[j][p] = buf_load16_once(rw, vw[p], 2u * k0);
+#pragma unroll
+    for (int p = 0; p < AP; ++p) areg[j][p] = buf_load16(rh, va[p], 2u * k0);
+  };
+  auto store_stage = [&](int j, int st) {
+    uint4* sp = smem + st * STAGE_Q;
+#pragma unroll
+    for (int p = 0; p < WP; ++p) sp[gran((tid >> 3) + (NT / 8) * p, tid & 7)] = wreg[j][p];
 #pragma unroll
     for (int p = 0; p < AP; ++p) {
-      const int idx = tid + LM_NT * p;
-      const int r = idx >> 3, g = idx & 7;
-      areg[p] = (r < MR && r < B)
-                    ? buf_load16(rh, 2u * (static_cast<uint32_t>(r) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * g), 0u)
-                    : make_uint4(0, 0, 0, 0);
+      const int idx = tid + NT * p;
+      if ((idx >> 3) < MR) sp[gran(TILE + (idx >> 3), idx & 7)] = areg[j][p];
     }
   };
-  auto store_stage = [&](int st) {
-    uint4* s = smem + st * STAGE_Q;
-#pragma unroll
-    for (int p = 0; p < WP; ++p) s[gran((tid >> 3) + 32 * p, tid & 7)] = wreg[p];
-#pragma unroll
-    for (int p = 0; p < AP; ++p) {
-      const int idx = tid + LM_NT * p;
-      if ((idx >> 3) < MR) s[gran(TILE + (idx >> 3), idx & 7)] = areg[p];
-    }
-  };
-
-  // Pipeline: iteration `it` multiplies stage it from LDS, stores stage it + 1
-  // (loaded during it - 1) into the other buffer and loads stage it + 2.
-  const int NIT = D / LM_KC;
-  load_stage(0);
-  store_stage(0);
-  if (NIT > 1) load_stage(LM_KC);
-  __syncthreads();
-  for (int it = 0; it < NIT; ++it) {
-    const int st = it & 1;
-    const uint4* s = smem + st * STAGE_Q;
+  auto compute = [&](int st) {
+    const uint4* sp = smem + st * STAGE_Q;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 bfr[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
-        bfr[nb] = __builtin_bit_cast(bf16x8, s[gran(64 * w + 16 * nb + l16, 4 * ks + l4)]);
+        bfr[nb] = __builtin_bit_cast(bf16x8, sp[gran(RW * w + 16 * nb + l16, 4 * ks + l4)]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const bf16x8 af = __builtin_bit_cast(bf16x8, s[gran(TILE + 16 * mb + l16, 4 * ks + l4)]);
+        const bf16x8 af = __builtin_bit_cast(bf16x8, sp[gran(TILE + 16 * mb + l16, 4 * ks + l4)]);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[nb], acc[mb][nb], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);   // (one step's fragments live at a time)
     }
-    if (it + 1 < NIT) {
-      store_stage(st ^ 1);
-      if (it + 2 < NIT) load_stage((it + 2) * LM_KC);
+  };
+
+  // Pipeline: stage s lives in register slot s % NSL and LDS buffer s & 1.
+  // Iteration `it` stores stage it + 1 (loaded NSL iterations earlier) into
+  // the buffer the previous iteration read, loads stage it + 1 + NSL into the
+  // slot it leaves, then multiplies stage it from LDS: NSL stages stream from
+  // HBM during each iteration.  Every load is issued unconditionally, in
+  // stage order (past the last stage, the last stage again, never stored),
+  // and the iterations run in whole groups of U (those past the last stage
+  // only load), so the wait before a store leaves the younger stages in
+  // flight.
+  // lane i of wave w: row w + NW i's bound, for the candidates after the loop
+  constexpr int RPW = MR / NW;
+  static_assert(RPW >= 1 && RPW <= WAVE, "rows per wave");
+  bool use_i = false;
+  uint32_t thr_i = 0;
+  if (lane < RPW && w + NW * lane < B) {
+    const int K = a.top_k[w + NW * lane];
+    use_i = K >= 1 && K <= FL_LM_HEAD_MAX_TOPK;
+    thr_i = use_i ? ws.thr[w + NW * lane] : 0u;
+  }
+
+  const int NIT = D / LM_KC;
+  const int NPAD = (NIT + U - 1) / U * U;
+  auto kc = [&](int st) { return min(st, NIT - 1) * LM_KC; };
+#pragma unroll
+  for (int j = 0; j < NSL; ++j) load_stage(j, kc(j));
+  store_stage(0, 0);
+  load_stage(0, kc(NSL));
+  __syncthreads();
+  for (int it0 = 0; it0 < NPAD; it0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int it = it0 + u;
+      if (it + 1 < NIT) store_stage((u + 1) % NSL, (u + 1) & 1);
+      load_stage((u + 1) % NSL, kc(it + 1 + NSL));
+      if (it < NIT) compute(u & 1);
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // ---------------- epilogue: keys of the tile (LDS reused), then per row the
@@ -432,59 +516,120 @@ __global__ __launch_bounds__(LM_NT) void k_lm_gemm(const fl_lm_head_args a, LmWs
   lm_epilogue<MB, NB, SC, true>(
       a, ws, acc,
       [&](int nb) {
-        const int n = e0 + 64 * w + 16 * nb + l16;
+        const int n = e0 + RW * w + 16 * nb + l16;
         return n < V ? n : -1;
       },
-      [&](int m, int nb, uint32_t key) { sKey[m][64 * w + 16 * nb + l16] = static_cast<uint16_t>(key); });
+      [&](int m, int nb, uint32_t key) { sKey[m][RW * w + 16 * nb + l16] = static_cast<uint16_t>(key); });
   __syncthreads();
-  const int rows = min(B, MR);
-  for (int m = w; m < rows; m += LM_NT / WAVE) {
-    const int K = a.top_k[m];
-    if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) continue;
-    const uint32_t thr = ws.thr[m];
-    uint64_t sel[4];
-    uint32_t k4[4];
+  // pass 1: per row, the count of the tile's keys at or above its bound
+  // (lane i counts row w + NW i); the rows' slots are then claimed by every
+  // lane at once
+  uint32_t cnt_i = 0;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int m = w + NW * i;
+    const uint32_t thr = static_cast<uint32_t>(__shfl(static_cast<int>(thr_i), i, WAVE));
+    if (m >= B || !__shfl(static_cast<int>(use_i), i, WAVE)) continue;
     int total = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      k4[q] = sKey[m][lane + WAVE * q];
-      sel[q] = __ballot(k4[q] != 0u && k4[q] >= thr);
-      total += __popcll(sel[q]);
+      const uint32_t k = sKey[m][lane + WAVE * q];
+      total += __popcll(__ballot(k != 0u && k >= thr));
     }
-    if (total == 0) continue;
-    uint32_t base = 0;
-    if (lane == 0) base = atomicAdd(&ws.cnt[m], static_cast<uint32_t>(total));
-    base = static_cast<uint32_t>(__shfl(static_cast<int>(base), 0, WAVE));
+    if (lane == i) cnt_i = static_cast<uint32_t>(total);
+  }
+  uint32_t base_i = 0;
+  if (cnt_i > 0) base_i = atomicAdd(&ws.cnt[(w + NW * lane) * LM_CNT_LD], cnt_i);
+  // pass 2: the candidates, (key << 32) | ~vocabulary index, in tile order
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int m = w + NW * i;
+    if (!__shfl(static_cast<int>(cnt_i), i, WAVE)) continue;
+    const uint32_t thr = static_cast<uint32_t>(__shfl(static_cast<int>(thr_i), i, WAVE));
+    uint32_t pos = static_cast<uint32_t>(__shfl(static_cast<int>(base_i), i, WAVE));
     uint64_t* cand = ws.cand + static_cast<size_t>(m) * LM_CAP;
-    const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t pos = base;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      if ((sel[q] >> lane) & 1ull) {
-        const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel[q] & below));
+      const uint32_t k = sKey[m][lane + WAVE * q];
+      const uint64_t sel = __ballot(k != 0u && k >= thr);
+      if ((sel >> lane) & 1ull) {
+        const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel & below));
         const uint32_t n = static_cast<uint32_t>(e0 + lane + WAVE * q);
-        if (p < static_cast<uint32_t>(LM_CAP)) cand[p] = (static_cast<uint64_t>(k4[q]) << 32) | static_cast<uint32_t>(~n);
+        if (p < static_cast<uint32_t>(LM_CAP)) cand[p] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~n);
       }
-      pos += static_cast<uint32_t>(__popcll(sel[q]));
+      pos += static_cast<uint32_t>(__popcll(sel));
     }
   }
 }
 
 // ---------------------------------------------------------------- thresh
 // The K-th largest of the row's sampled keys (0 when fewer than K were
-// sampled): the keys into LDS, then the radix select of wave 0.
+// sampled), and the row's counters.  The keys go into LDS in 16-byte pieces;
+// two passes of a 256-bin histogram follow (high byte, then the low byte
+// within the chosen high byte), every wave counting into a histogram of its
+// own, and wave 0 finds the bin.
 __global__ __launch_bounds__(LM_NT) void k_lm_thresh(const fl_lm_head_args a, LmWs ws) {
-  __shared__ uint16_t keys[LM_NSAMPLE];
-  __shared__ uint32_t hist[256];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  constexpr int NW = LM_NT / WAVE;
+  __shared__ uint4 keys[LM_NSAMPLE / 8];
+  __shared__ uint32_t hist[NW][256];
+  __shared__ int s_bin;
+  __shared__ uint32_t s_above;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
+  if (tid == 0) {
+    ws.cnt[b * LM_CNT_LD] = 0u;
+    ws.thr[b] = 0u;
+    if (!ws.prep) ws.stat[b] = 0u;
+  }
   const int K = a.top_k[b];
   if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) return;   // (the pick reports the row)
-  const uint16_t* src = ws.skey + static_cast<size_t>(b) * ws.ns;
-  for (int i = tid; i < ws.ns; i += LM_NT) keys[i] = src[i];
-  __syncthreads();
-  if (tid >= WAVE) return;
-  const uint32_t t = wave_kth_key(ws.ns, K, hist, [&](int i) { return static_cast<uint32_t>(keys[i]); });
-  if (tid == 0) ws.thr[b] = t;
+  const int ns = ws.ns, nq = (ns + 7) >> 3;
+  const uint4* src = reinterpret_cast<const uint4*>(ws.skey + static_cast<size_t>(b) * ws.nsl);
+  for (int i = tid; i < nq; i += LM_NT) keys[i] = src[i];
+  int k = K;
+  uint32_t prefix = 0;   // high byte, once chosen
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int i = tid; i < NW * 256; i += LM_NT) (&hist[0][0])[i] = 0u;
+    __syncthreads();   // (pass 0: also the keys)
+    for (int i = tid; i < nq; i += LM_NT) {
+      const uint4 q = keys[i];
+      const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+      const int nj = min(8, ns - 8 * i);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t key = (wd[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+        if (j < nj) {
+          if (pass == 0) atomicAdd(&hist[w][key >> 8], 1u);
+          else if ((key >> 8) == prefix) atomicAdd(&hist[w][key & 0xFFu], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      uint32_t c4[4], above = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) c += hist[v][255 - 4 * lane - q];
+        c4[q] = c;
+      }
+      const int bin = wave_top_bin(c4, k, above);
+      if (lane == 0) {
+        s_bin = bin;
+        s_above = above;
+      }
+    }
+    __syncthreads();
+    const int bin = s_bin;
+    if (bin < 0) return;   // fewer than K keys: no bound (thr stays 0)
+    k -= static_cast<int>(s_above);
+    if (pass == 0) {
+      prefix = static_cast<uint32_t>(bin);
+    } else if (tid == 0) {
+      ws.thr[b] = (prefix << 8) | static_cast<uint32_t>(bin);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- pick
@@ -532,7 +677,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick(const fl_lm_head_args a, LmWs
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (WAVE - 1);
   uint32_t status = ws.stat[b];
   const int K = a.top_k[b];
-  const uint32_t nc = ws.cnt[b];
+  const uint32_t nc = ws.cnt[b * LM_CNT_LD];
   if (K < 1 || K > FL_LM_HEAD_MAX_TOPK || nc > static_cast<uint32_t>(LM_CAP)) status |= FL_ROW_LIMIT;
   if (tid == 0) {
     s_n = 0;
@@ -689,9 +834,10 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick(const fl_lm_head_args a, LmWs
 size_t lm_head_workspace_bytes(int64_t batch, int64_t vocab) { return lm_ws_bytes(batch, vocab); }
 
 hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s) {
-  const LmWs ws = lm_ws(a.workspace, a.batch, a.vocab);
+  LmWs ws = lm_ws(a.workspace, a.batch, a.vocab);
+  ws.prep = a.repetition_penalty != nullptr && a.hist_ids != nullptr && a.hist_len != nullptr;
   const dim3 rows(static_cast<unsigned>(a.batch));
-  hipLaunchKernelGGL(k_lm_prep, rows, dim3(LM_NT), 0, s, a, ws);
+  if (ws.prep) hipLaunchKernelGGL(k_lm_prep, rows, dim3(LM_NT), 0, s, a, ws);
   const dim3 stiles(static_cast<unsigned>((ws.ns + 63) / 64));
   const dim3 tiles(static_cast<unsigned>((a.vocab + 255) / 256));
   const bool sc = a.softcap > 0.0f;
@@ -701,7 +847,7 @@ hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s) {
     constexpr bool SC = decltype(tag_sc)::value;
     hipLaunchKernelGGL((k_lm_sample<MB, SC>), stiles, dim3(LM_NT), 0, s, a, ws);
     hipLaunchKernelGGL(k_lm_thresh, rows, dim3(LM_NT), 0, s, a, ws);
-    hipLaunchKernelGGL((k_lm_gemm<MB, SC>), tiles, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_gemm<MB, SC, LM_GW>), tiles, dim3(LM_GW * WAVE), 0, s, a, ws);
   };
   using T1 = std::integral_constant<int, 1>;
   using T2 = std::integral_constant<int, 2>;

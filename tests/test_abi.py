@@ -258,9 +258,10 @@ def test_lm_head_argument_errors():
         setattr(a, f, 0x10000)
     n = ctypes.c_size_t(0)
     assert L.fl_lm_head_workspace_bytes(4, 1000, ctypes.byref(n)) == _lib.FL_OK
-    # three int32 arrays (256-byte aligned), a 32-word bitmap per row, 4096 candidates per row
-    # (+ the keys of the sampled rows: all 1000 rows at this vocabulary size, 2 bytes each, 256-byte aligned)
-    assert n.value == 3 * 256 + 512 + 8192 + 8 * 4 * 4096
+    # two int32 arrays (256-byte aligned), a counter per 256 bytes, a 32-word bitmap per row,
+    # 4096 candidates per row (+ the keys of the sampled rows: all 1000 rows at this vocabulary
+    # size, 2 bytes each, 256-byte aligned)
+    assert n.value == 2 * 256 + 4 * 256 + 512 + 8192 + 8 * 4 * 4096
     assert L.fl_lm_head_workspace_bytes(65, 1000, ctypes.byref(n)) == _lib.FL_EINVAL
     a.workspace, a.workspace_bytes = 0x100000, n.value
     cases = [(dict(dtype=_lib.FL_DTYPE_F32), _lib.FL_ENOTSUP, "bf16"),
