@@ -41,15 +41,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int LM_NT = 256;                 // threads of the gemm and pick work-groups
 constexpr int LM_NTILE = 256;              // vocabulary rows per gemm tile
-#ifndef LM_GW
-#define LM_GW 8
-#endif
-#ifndef LM_GSLOTS
-#define LM_GSLOTS 2
-#endif
+constexpr int LM_GW = 8;                   // waves per main-gemm work-group (32 vocabulary rows each)
+constexpr int LM_GSLOTS = 2;               // main-gemm stages in flight (register slots)
+
 constexpr int LM_KC = 64;                  // dim per pipeline stage (two MFMA steps of 32)
 constexpr int LM_AST = LM_KC + 8;          // LDS row stride of a hidden-state stage, bf16 elements
-constexpr int LM_NST = 8;                  // weight stages in flight per wave of the sample gemm
 constexpr int LM_NSAMPLE = 8192;           // sampled vocabulary rows (at most)
 constexpr int LM_CAP = FL_LM_HEAD_MAX_CAND;
 // Every gemm tile adds its candidate count to each row's counter at the end
@@ -62,9 +58,46 @@ constexpr int LM_CNT_LD = 64;
 // 0 only for the all-ones NaN pattern (the epilogue maps every NaN to 0).
 __device__ __forceinline__ uint32_t asc16(uint32_t bits) { return 0xFFFFu - order16(bits); }
 __device__ __forceinline__ uint32_t bits_of_asc16(uint32_t k) { return bits_of_order16(0xFFFFu - k); }
+// asc16 keys of -inf and +inf: the non-NaN patterns are exactly the keys
+// between them (-NaN patterns lie below, +NaN above)
+constexpr uint32_t LM_KEY_NINF = 0x007Fu, LM_KEY_PINF = 0xFF80u;
+constexpr uint32_t LM_KEY_NONE = 0x10000u;   // a threshold no key reaches
+__device__ __forceinline__ bool bf16_nan(uint32_t bits) { return (bits & 0x7FFFu) > 0x7F80u; }
+
+// A logit's value after soft-cap (cap > 0), the penalty (history members)
+// and temperature, as fl_sample evaluates them on a bf16 row, from the
+// logit's bf16 pattern.
+__device__ __forceinline__ float lm_tval(uint32_t bits, float cap, bool member, float RP, float T, float RT) {
+  float z = BF16::to_f32(bits);
+  if (cap > 0.0f) z = softcap_val<BF16>(z, cap);
+  if (member) z = penalty_val<BF16>(z, RP);
+  return temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
+}
+__device__ __forceinline__ uint32_t lm_key_of(float y) { return y != y ? 0u : asc16(BF16::from_f32(y)); }
+
+// Smallest key r in [lo, hi] with pred(r) (hi + 1 when none), for pred false
+// then true along r; one wave, 64 keys tested per round.
+template <class P>
+__device__ uint32_t wave_first_key(uint32_t lo, uint32_t hi, P&& pred) {
+  const uint32_t lane = threadIdx.x & (WAVE - 1);
+  uint32_t end = hi + 1;   // the answer lies in [lo, end]; end: none, or a key known to pass
+  while (lo < end) {
+    const uint32_t step = (end - lo + WAVE - 1) / WAVE;
+    const uint32_t r = lo + step * lane;
+    const uint64_t m = __ballot(r < end && pred(r));
+    if (m == 0) {
+      lo += step * min(static_cast<uint32_t>(WAVE - 1), (end - 1 - lo) / step) + 1;
+    } else {
+      const uint32_t j = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(m)) - 1);
+      end = lo + step * j;
+      if (j > 0) lo += step * (j - 1) + 1;
+    }
+  }
+  return end;
+}
 
 struct LmWs {
-  uint32_t* thr;    // [batch] the row's bound (asc16 key; 0: none)
+  uint32_t* rthr;   // [batch, 4] raw-key thresholds: candidates (non-member, member), +inf (non-member, member)
   uint32_t* cnt;    // [batch, LM_CNT_LD] candidates appended (word 0 of a row's 256 bytes)
   uint32_t* stat;   // [batch] FL_ROW_* bits found by prep and gemm
   uint32_t* bits;   // [batch, bw] history bitmap
@@ -88,7 +121,7 @@ __host__ __device__ inline int lm_bw(int64_t vocab) { return static_cast<int>(((
 __host__ __device__ inline int lm_nsl(int64_t vocab) { return (lm_ns(vocab) + 7) & ~7; }
 __host__ __device__ inline size_t lm_ws_bytes(int64_t batch, int64_t vocab) {
   const size_t B = static_cast<size_t>(batch), bw = static_cast<size_t>(lm_bw(vocab));
-  return 2 * lm_align(4 * B) + 4 * B * LM_CNT_LD + lm_align(4 * B * bw) +
+  return lm_align(16 * B) + lm_align(4 * B) + 4 * B * LM_CNT_LD + lm_align(4 * B * bw) +
          lm_align(2 * B * static_cast<size_t>(lm_nsl(vocab))) + 8 * B * LM_CAP;
 }
 inline LmWs lm_ws(void* p, int64_t batch, int64_t vocab) {
@@ -101,8 +134,8 @@ inline LmWs lm_ws(void* p, int64_t batch, int64_t vocab) {
   w.nsl = lm_nsl(vocab);
   w.prep = 0;
   size_t off = 0;
-  w.thr = reinterpret_cast<uint32_t*>(q + off);
-  off += lm_align(4 * B);
+  w.rthr = reinterpret_cast<uint32_t*>(q + off);
+  off += lm_align(16 * B);
   w.cnt = reinterpret_cast<uint32_t*>(q + off);
   off += 4 * B * LM_CNT_LD;
   w.stat = reinterpret_cast<uint32_t*>(q + off);
@@ -175,20 +208,20 @@ __device__ uint32_t wave_kth_key(int n, int k, uint32_t* hist, KeyAt&& key_at) {
 // ---------------------------------------------------------------- prep
 // Launched when the call passes a penalty and histories; one work-group per
 // row.  A penalised row gets its history bitmap (one bit per vocabulary id,
-// which also de-duplicates the ids); every row gets its status from its
-// history (too long, ids out of range).
+// which also de-duplicates the ids), built in LDS and written out whole;
+// every row gets its status from its history (too long, ids out of range).
 __global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs ws) {
+  __shared__ __attribute__((aligned(16))) uint32_t sbits[FL_MAX_VOCAB_16 / 32];   // (bw <= this)
   __shared__ uint32_t s_flags;
   const int b = blockIdx.x, tid = threadIdx.x;
-  uint32_t* bits = ws.bits + static_cast<size_t>(b) * ws.bw;
   const bool pen = row_penalised(a, b);
   if (tid == 0) s_flags = 0u;
+  int H = pen ? a.hist_len[b] : 0;
   if (pen) {
-    uint4* b4 = reinterpret_cast<uint4*>(bits);
+    uint4* b4 = reinterpret_cast<uint4*>(sbits);
     for (int i = tid; i < ws.bw / 4; i += LM_NT) b4[i] = make_uint4(0u, 0u, 0u, 0u);
   }
-  __syncthreads();  // (the bitmap's zeros reach memory before the atomics below)
-  int H = pen ? a.hist_len[b] : 0;
+  __syncthreads();
   if (H > FL_MAX_HISTORY) {
     if (tid == 0) s_flags = static_cast<uint32_t>(FL_ROW_LIMIT);
     H = 0;
@@ -201,92 +234,68 @@ __global__ __launch_bounds__(LM_NT) void k_lm_prep(const fl_lm_head_args a, LmWs
   for (int i = tid; i < H; i += LM_NT) {
     const int id = hid[i];
     if (id < 0 || id >= a.vocab) atomicOr(&s_flags, static_cast<uint32_t>(FL_ROW_BAD_HISTORY));
-    else atomicOr(&bits[id >> 5], 1u << (id & 31));
+    else atomicOr(&sbits[id >> 5], 1u << (id & 31));
   }
   __syncthreads();
+  if (pen) {
+    uint4* dst = reinterpret_cast<uint4*>(ws.bits + static_cast<size_t>(b) * ws.bw);
+    const uint4* b4 = reinterpret_cast<const uint4*>(sbits);
+    for (int i = tid; i < ws.bw / 4; i += LM_NT) dst[i] = b4[i];
+  }
   if (tid == 0) ws.stat[b] = s_flags;
 }
 
-// ---------------------------------------------------------------- gemm epilogue
-// One lane's logits after its MFMA chains: acc[mb][nb][r] is batch row
-// 16 mb + 4 l4 + r and vocabulary row col(nb) (negative: past the end).  Each
-// value is rounded to bf16 (the logit; stored to out_logits by the main gemm),
-// then soft-capped, penalised and divided by the temperature as fl_sample
-// does; put(m, nb, key) receives its order key (0 for NaN and out of range).
-// The main gemm also records NaN and +inf values in the row's status.
-// Two phases: first every key, with loads only (the rows' parameters and
-// history bits), then every store.  Global stores among the loads would keep
-// the compiler from issuing a later row's loads before an earlier row's
-// stores, one memory round trip per row.
-template <int MB, int NB, bool SC, bool MAIN, class Col, class Put>
-__device__ __forceinline__ void lm_epilogue(const fl_lm_head_args& a, const LmWs& ws, const floatx4 (&acc)[MB][NB],
-                                            Col&& col, Put&& put) {
-  const int l4 = (threadIdx.x & (WAVE - 1)) >> 4;
-  const int B = static_cast<int>(a.batch), V = static_cast<int>(a.vocab);
-  const float cap = a.softcap;
-  uint32_t key[MB][4][NB], flags[MB][4];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * mb + 4 * l4 + r;
-      const bool row_ok = m < B;
-      const int mc = row_ok ? m : 0;
-      const float T = a.temperature[mc];
-      const float RT = T > 0.0f ? 1.0f / T : 0.0f;
-      const bool pen = row_ok && row_penalised(a, mc);
-      const float RP = pen ? a.repetition_penalty[mc] : 1.0f;
-      const uint32_t* hb = ws.bits + static_cast<size_t>(mc) * ws.bw;
-      uint32_t f = 0;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int n = col(nb);
-        const bool ok = row_ok && n >= 0;
-        float z = BF16::to_f32(BF16::from_f32(acc[mb][nb][r]));
-        if constexpr (SC) z = softcap_val<BF16>(z, cap);
-        if (pen && ok && ((hb[n >> 5] >> (n & 31)) & 1u)) z = penalty_val<BF16>(z, RP);
-        const float y = temperature_val<BF16>(z, T, RT) + 0.0f;  // (+0.0f: -0 and +0 share a key)
-        const uint32_t yb = BF16::from_f32(y);
-        const bool nan = y != y;
-        f |= (ok && nan) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u;
-        f |= (ok && y == __builtin_inff()) ? static_cast<uint32_t>(FL_ROW_INF) : 0u;
-        key[mb][r][nb] = (ok && !nan) ? asc16(yb) : 0u;
-      }
-      flags[mb][r] = f;
-    }
+// ---------------------------------------------------------------- row parameters
+// The sample gemm's rows' parameters in LDS, filled once per work-group
+// (thread m loads row m's before the gemm's loop, into registers, and stores
+// them to LDS after it), so its epilogue computes every key without a memory
+// round trip.
+template <int MR>
+struct LmRows {
+  float T[MR], RT[MR], RP[MR];   // temperature, RN(1 / T) (0 for greedy), penalty (1: none)
+  uint32_t pen[MR];              // the row is penalised
+};
+struct LmRowReg {
+  float T, RP;
+  uint32_t pen;
+};
+__device__ __forceinline__ LmRowReg lm_row_load(const fl_lm_head_args& a, int m) {
+  LmRowReg r{1.0f, 1.0f, 0u};
+  if (m < a.batch) {
+    r.T = a.temperature[m];
+    r.pen = row_penalised(a, m) ? 1u : 0u;
+    r.RP = r.pen ? a.repetition_penalty[m] : 1.0f;
   }
-  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * mb + 4 * l4 + r;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        put(m, nb, key[mb][r][nb]);
-        const int n = col(nb);
-        if (MAIN && out_logits != nullptr && m < B && n >= 0)
-          out_logits[static_cast<int64_t>(m) * V + n] = static_cast<uint16_t>(BF16::from_f32(acc[mb][nb][r]));
-      }
-      if (MAIN && flags[mb][r]) atomicOr(&ws.stat[m], flags[mb][r]);
-    }
-  }
+  return r;
+}
+template <int MR>
+__device__ __forceinline__ void lm_row_store(LmRows<MR>& p, int m, const LmRowReg& r) {
+  p.T[m] = r.T;
+  p.RT[m] = r.T > 0.0f ? 1.0f / r.T : 0.0f;
+  p.RP[m] = r.RP;
+  p.pen[m] = r.pen;
 }
 
 // ---------------------------------------------------------------- sample gemm
 // The sampled rows: vocabulary rows e·S for tile entries e, 16 per wave and 64
-// per work-group (ns / 64 work-groups), keys stored to ws.skey.  MB: 16-row
-// blocks of the batch (1, 2 or 4).  SC: a soft-cap.  Each 16 x 16 block of
-// logits is one wave's MFMA chain over the dim in 32-wide steps in ascending
-// order, as in the main gemm below, so a sampled value equals the main gemm's
-// value of the same logit bit for bit.
-template <int MB, bool SC>
+// per work-group (ns / 64 work-groups), the keys of their transformed values
+// stored to ws.skey.  MB: 16-row blocks of the batch (1, 2 or 4).  Each
+// 16 x 16 block of logits is one wave's MFMA chain over the dim in 32-wide
+// steps in ascending order, as in the main gemm below, so a sampled value
+// equals the main gemm's value of the same logit bit for bit.
+template <int MB>
 __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, LmWs ws) {
+  constexpr int NST = 8;                            // register slots (stages in flight)
+  constexpr int MR = 16 * MB;
+  constexpr int NE = 16 * (LM_NT / WAVE);          // sampled entries per work-group
+  constexpr int BP = MR * NE / LM_NT;              // history words per thread
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][16 * MB * LM_AST];
+  __shared__ LmRows<MR> sRows;
+  __shared__ uint32_t sBits[MR][NE];                // word of entry j's vocabulary row in row m's bitmap
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
   const int B = static_cast<int>(a.batch), D = static_cast<int>(a.dim);
   const int S = ws.stride, ns = ws.ns;
-  const int e0 = blockIdx.x * (LM_NT / WAVE) * 16;
+  const int e0 = blockIdx.x * NE;
   const int l16 = lane & 15, l4 = lane >> 4;
   const uint16_t* W = static_cast<const uint16_t*>(a.weight);
   // hidden rows 0 .. B-1 (rows of the last block past B read zeros)
@@ -304,12 +313,13 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
   const uint16_t* wp = W + static_cast<int64_t>(min(eme, ns - 1)) * S * D + 8 * l4;
   // hidden-state stage: 16 MB rows x 64 columns = 128 MB pieces of 16 bytes
   // (pieces of rows past the batch lie past the buffer's range and read zeros)
-  constexpr int APIECES = (16 * MB * LM_KC / 8 + LM_NT - 1) / LM_NT;
+  constexpr int GS = LM_KC / 8;
+  constexpr int APIECES = (16 * MB * GS + LM_NT - 1) / LM_NT;
   auto load_a = [&](uint4 (&ap)[APIECES], int k0) {
 #pragma unroll
     for (int s = 0; s < APIECES; ++s) {
       const int idx = tid + LM_NT * s;
-      const int row = idx >> 3, seg = idx & 7;
+      const int row = idx / GS, seg = idx % GS;
       ap[s] = buf_load16(rh, 2u * (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.ld_hidden) + k0 + 8 * seg), 0u);
     }
   };
@@ -317,7 +327,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
 #pragma unroll
     for (int s = 0; s < APIECES; ++s) {
       const int idx = tid + LM_NT * s;
-      const int row = idx >> 3, seg = idx & 7;
+      const int row = idx / GS, seg = idx % GS;
       if (row < 16 * MB) *reinterpret_cast<uint4*>(&sA[st][row * LM_AST + 8 * seg]) = ap[s];
     }
   };
@@ -336,42 +346,79 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
     }
   };
 
+  // the rows' parameters and, for a penalty, the history words of the
+  // tile's sampled rows, loaded now and put into LDS after the loop
+  const LmRowReg rowp = lm_row_load(a, tid);
+  uint32_t bitp[BP];
+#pragma unroll
+  for (int q = 0; q < BP; ++q) {
+    const int i = tid + LM_NT * q, m = i / NE, j = i % NE;
+    const int e = min(e0 + j, ns - 1);
+    bitp[q] = (ws.prep && m < B) ? ws.bits[static_cast<size_t>(m) * ws.bw + ((e * S) >> 5)] : 0u;
+  }
+
   // Pipeline: stage s (its weight fragments and its hidden pieces) lives in
-  // register slot s % LM_NST.  Iteration `it` stores the hidden pieces of
-  // stage it + 1 into LDS buffer (it + 1) & 1, multiplies stage it, and refills
-  // its slot with stage it + LM_NST, so LM_NST - 1 stages stream from memory
-  // during each iteration.  Every load is issued unconditionally, in stage
-  // order (past the last stage, the last stage again, never used), and the
-  // iterations run in whole groups of LM_NST (those past the last stage only
+  // register slot s % NST.  Iteration `it` stores the hidden pieces of stage
+  // it + 1 into LDS buffer (it + 1) & 1, multiplies stage it, and refills its
+  // slot with stage it + NST, so NST - 1 stages stream from memory during
+  // each iteration.  Every load is issued unconditionally, in stage order
+  // (past the last stage, the last stage again, never used), and the
+  // iterations run in whole groups of NST (those past the last stage only
   // load), so the waits before the LDS stores and the MFMAs leave the later
   // stages in flight.
   const int NIT = D / LM_KC;
-  const int NPAD = (NIT + LM_NST - 1) / LM_NST * LM_NST;
+  const int NPAD = (NIT + NST - 1) / NST * NST;
   auto kc = [&](int st) { return min(st, NIT - 1) * LM_KC; };
-  uint4 wr[LM_NST][2], ar[LM_NST][APIECES];
+  uint4 wr[NST][2], ar[NST][APIECES];
 #pragma unroll
-  for (int u = 0; u < LM_NST; ++u) {
+  for (int u = 0; u < NST; ++u) {
     load_w(wr[u], kc(u));
     load_a(ar[u], kc(u));
   }
   store_a(ar[0], 0);
   __syncthreads();
-  for (int it0 = 0; it0 < NPAD; it0 += LM_NST) {
+  for (int it0 = 0; it0 < NPAD; it0 += NST) {
 #pragma unroll
-    for (int u = 0; u < LM_NST; ++u) {
+    for (int u = 0; u < NST; ++u) {
       const int it = it0 + u;
-      if (it + 1 < NIT) store_a(ar[(u + 1) % LM_NST], (it + 1) & 1);
+      if (it + 1 < NIT) store_a(ar[(u + 1) % NST], (it + 1) & 1);
       if (it < NIT) mfma_stage(it & 1, wr[u]);
-      load_w(wr[u], kc(it + LM_NST));
-      load_a(ar[u], kc(it + LM_NST));
+      load_w(wr[u], kc(it + NST));
+      load_a(ar[u], kc(it + NST));
       __syncthreads();
     }
   }
-  lm_epilogue<MB, 1, SC, false>(
-      a, ws, acc, [&](int) { return eme < ns ? eme * S : -1; },
-      [&](int m, int, uint32_t key) {
-        if (m < B && eme < ns) ws.skey[static_cast<size_t>(m) * ws.nsl + eme] = static_cast<uint16_t>(key);
-      });
+  if (tid < MR) lm_row_store(sRows, tid, rowp);
+#pragma unroll
+  for (int q = 0; q < BP; ++q) {
+    const int i = tid + LM_NT * q;
+    sBits[i / NE][i % NE] = bitp[q];
+  }
+  __syncthreads();
+  // the sampled values' keys: bf16 rounding (the logit), then soft-cap,
+  // penalty and temperature (lm_tval, as the thresholds and the pick apply them)
+  const float cap = a.softcap;
+  const int n = eme * S;
+  uint32_t key[MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+      const bool ok = m < B && eme < ns;
+      const bool member = ok && sRows.pen[m] != 0u && ((sBits[m][16 * w + l16] >> (n & 31)) & 1u);
+      const float y = lm_tval(BF16::from_f32(acc[mb][0][r]), cap, member, sRows.RP[m], sRows.T[m], sRows.RT[m]);
+      key[mb][r] = ok ? lm_key_of(y) : 0u;
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+      if (m < B && eme < ns) ws.skey[static_cast<size_t>(m) * ws.nsl + eme] = static_cast<uint16_t>(key[mb][r]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- main gemm
@@ -385,7 +432,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_sample(const fl_lm_head_args a, Lm
 // LDS holds 16-byte granule g of row r at r·8 + (g xor ((r >> 1) & 7)): the
 // fragment reads (16 rows, one granule column) and the stores (8 granules of
 // one row) then spread over all banks.
-template <int MB, bool SC, int NW>
+template <int MB, int NW>
 __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 2))) void k_lm_gemm(const fl_lm_head_args a,
                                                                                                    LmWs ws) {
   constexpr int NT = NW * WAVE;
@@ -394,7 +441,9 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 
   constexpr int NB = RW / 16;                     // 16-row weight blocks per wave
   constexpr int MR = 16 * MB;                     // batch rows of the tile
   constexpr int STAGE_Q = (TILE + MR) * 8;        // 16-byte granules per stage
-  constexpr int KEY_Q = (MR * TILE * 2 + 15) / 16;
+  constexpr int KEYB = MR * TILE * 2;              // epilogue LDS: keys, row parameters, history words
+  constexpr int KEY_Q = (KEYB + MR * 16 + MR * 4 + MR * 8 * 4 + 15) / 16;
+  static_assert(KEYB % 16 == 0 && MR * 8 <= NT, "epilogue LDS");
   constexpr int SMEM_Q = (2 * STAGE_Q > KEY_Q) ? 2 * STAGE_Q : KEY_Q;
   static_assert(TILE == 16 * NB * NW && LM_KC == 64 && TILE * 8 % NT == 0, "stage shape");
   __shared__ __attribute__((aligned(16))) uint4 smem[SMEM_Q];
@@ -480,15 +529,21 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 
   // and the iterations run in whole groups of U (those past the last stage
   // only load), so the wait before a store leaves the younger stages in
   // flight.
-  // lane i of wave w: row w + NW i's bound, for the candidates after the loop
-  constexpr int RPW = MR / NW;
+  // thread m < MR: row m's thresholds and whether it is penalised; thread
+  // t < 8 MR: word t & 7 of the tile's 8 history words of row t >> 3 (for a
+  // penalty); loaded now, put into LDS after the loop
+  constexpr int RPW = MR / NW;   // rows per wave in the candidate append
   static_assert(RPW >= 1 && RPW <= WAVE, "rows per wave");
-  bool use_i = false;
-  uint32_t thr_i = 0;
-  if (lane < RPW && w + NW * lane < B) {
-    const int K = a.top_k[w + NW * lane];
-    use_i = K >= 1 && K <= FL_LM_HEAD_MAX_TOPK;
-    thr_i = use_i ? ws.thr[w + NW * lane] : 0u;
+  uint4 rthr = make_uint4(LM_KEY_NONE, LM_KEY_NONE, LM_KEY_NONE, LM_KEY_NONE);
+  uint32_t rpen = 0;
+  if (tid < B) {
+    rthr = *reinterpret_cast<const uint4*>(ws.rthr + 4 * static_cast<size_t>(tid));
+    rpen = row_penalised(a, tid) ? 1u : 0u;
+  }
+  uint32_t bitw = 0;
+  {
+    const int m = tid >> 3, wd = (e0 >> 5) + (tid & 7);
+    if (ws.prep && tid < 8 * MR && m < B && wd < ws.bw) bitw = ws.bits[static_cast<size_t>(m) * ws.bw + wd];
   }
 
   const int NIT = D / LM_KC;
@@ -512,14 +567,70 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 
 
   // ---------------- epilogue: keys of the tile (LDS reused), then per row the
   // tile's keys at or above the bound appended to the row's candidates
-  uint16_t (*sKey)[TILE] = reinterpret_cast<uint16_t (*)[TILE]>(smem);
-  lm_epilogue<MB, NB, SC, true>(
-      a, ws, acc,
-      [&](int nb) {
-        const int n = e0 + RW * w + 16 * nb + l16;
-        return n < V ? n : -1;
-      },
-      [&](int m, int nb, uint32_t key) { sKey[m][RW * w + 16 * nb + l16] = static_cast<uint16_t>(key); });
+  char* lds = reinterpret_cast<char*>(smem);
+  uint16_t (*sKey)[TILE] = reinterpret_cast<uint16_t (*)[TILE]>(lds);
+  uint4* sThr = reinterpret_cast<uint4*>(lds + KEYB);
+  uint32_t* sPen = reinterpret_cast<uint32_t*>(lds + KEYB + MR * 16);
+  uint32_t (*sBits)[8] = reinterpret_cast<uint32_t (*)[8]>(lds + KEYB + MR * 16 + MR * 4);
+  if (tid < MR) {
+    sThr[tid] = rthr;
+    sPen[tid] = rpen;
+  }
+  if (tid < 8 * MR) sBits[tid >> 3][tid & 7] = bitw;
+  __syncthreads();
+  // Per value (batch row 16 mb + 4 l4 + r, tile column RW w + 16 nb + l16):
+  // its bf16 pattern, whether it is a candidate (the row's threshold for its
+  // class reached), and NaN or +inf results for the row's status; then the
+  // stores (candidate keys to LDS, the logits, the status bits).
+  static_assert(MB * 4 * NB <= 32 && NB % 2 == 0, "epilogue packing");
+  uint32_t bits2[MB][4][NB / 2];   // two bf16 patterns per word
+  uint32_t cand = 0;               // bit (mb·4 + r)·NB + nb
+  uint32_t fnan = 0, finf = 0;     // bit mb·4 + r
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+      const bool row_ok = m < B;
+      const uint4 th = sThr[m];
+      const bool pen = row_ok && sPen[m] != 0u;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int c = RW * w + 16 * nb + l16;
+        const bool ok = row_ok && e0 + c < V;
+        const uint32_t bits = BF16::from_f32(acc[mb][nb][r]);
+        if (nb & 1) bits2[mb][r][nb >> 1] |= bits << 16;
+        else bits2[mb][r][nb >> 1] = bits;
+        const bool nan = bf16_nan(bits);
+        const uint32_t kr = asc16(bits);
+        const bool member = pen && ((sBits[m][c >> 5] >> (c & 31)) & 1u);
+        const uint32_t tc = member ? th.y : th.x, ti = member ? th.w : th.z;
+        const int bit = (mb * 4 + r) * NB + nb;
+        cand |= (ok && !nan && kr >= tc) ? (1u << bit) : 0u;
+        fnan |= (ok && nan) ? (1u << (mb * 4 + r)) : 0u;
+        finf |= (ok && !nan && kr >= ti) ? (1u << (mb * 4 + r)) : 0u;
+      }
+    }
+  }
+  uint16_t* out_logits = static_cast<uint16_t*>(a.out_logits);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mb + 4 * l4 + r;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int c = RW * w + 16 * nb + l16;
+        const uint32_t bits = (bits2[mb][r][nb >> 1] >> (16 * (nb & 1))) & 0xFFFFu;
+        const bool cd = (cand >> ((mb * 4 + r) * NB + nb)) & 1u;
+        sKey[m][c] = static_cast<uint16_t>(cd ? asc16(bits) : 0u);
+        if (out_logits != nullptr && m < B && e0 + c < V) out_logits[static_cast<int64_t>(m) * V + e0 + c] = static_cast<uint16_t>(bits);
+      }
+      const uint32_t f = (((fnan >> (mb * 4 + r)) & 1u) ? static_cast<uint32_t>(FL_ROW_NAN) : 0u) |
+                         (((finf >> (mb * 4 + r)) & 1u) ? static_cast<uint32_t>(FL_ROW_INF) : 0u);
+      if (f) atomicOr(&ws.stat[m], f);
+    }
+  }
   __syncthreads();
   // pass 1: per row, the count of the tile's keys at or above its bound
   // (lane i counts row w + NW i); the rows' slots are then claimed by every
@@ -528,31 +639,26 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int m = w + NW * i;
-    const uint32_t thr = static_cast<uint32_t>(__shfl(static_cast<int>(thr_i), i, WAVE));
-    if (m >= B || !__shfl(static_cast<int>(use_i), i, WAVE)) continue;
+    if (m >= B) continue;
     int total = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t k = sKey[m][lane + WAVE * q];
-      total += __popcll(__ballot(k != 0u && k >= thr));
-    }
+    for (int q = 0; q < 4; ++q) total += __popcll(__ballot(sKey[m][lane + WAVE * q] != 0u));
     if (lane == i) cnt_i = static_cast<uint32_t>(total);
   }
   uint32_t base_i = 0;
   if (cnt_i > 0) base_i = atomicAdd(&ws.cnt[(w + NW * lane) * LM_CNT_LD], cnt_i);
-  // pass 2: the candidates, (key << 32) | ~vocabulary index, in tile order
+  // pass 2: the candidates, (raw key << 32) | ~vocabulary index, in tile order
   const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int m = w + NW * i;
     if (!__shfl(static_cast<int>(cnt_i), i, WAVE)) continue;
-    const uint32_t thr = static_cast<uint32_t>(__shfl(static_cast<int>(thr_i), i, WAVE));
     uint32_t pos = static_cast<uint32_t>(__shfl(static_cast<int>(base_i), i, WAVE));
     uint64_t* cand = ws.cand + static_cast<size_t>(m) * LM_CAP;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t k = sKey[m][lane + WAVE * q];
-      const uint64_t sel = __ballot(k != 0u && k >= thr);
+      const uint64_t sel = __ballot(k != 0u);
       if ((sel >> lane) & 1ull) {
         const uint32_t p = pos + static_cast<uint32_t>(__popcll(sel & below));
         const uint32_t n = static_cast<uint32_t>(e0 + lane + WAVE * q);
@@ -564,11 +670,18 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(NW / 
 }
 
 // ---------------------------------------------------------------- thresh
-// The K-th largest of the row's sampled keys (0 when fewer than K were
-// sampled), and the row's counters.  The keys go into LDS in 16-byte pieces;
-// two passes of a 256-bin histogram follow (high byte, then the low byte
-// within the chosen high byte), every wave counting into a histogram of its
-// own, and wave 0 finds the bin.
+// The row's bound, then its raw-key thresholds, and the row's counters.
+// The bound is the K-th largest of the row's sampled keys (none when fewer
+// than K were sampled): the keys go into LDS in 16-byte pieces, then two
+// passes of a 256-bin histogram (high byte, then the low byte within the
+// chosen high byte), every wave counting into a histogram of its own.
+// Soft-cap, penalty and temperature are monotone (non-decreasing) in the
+// logit, separately for history members and the rest, so "transformed key
+// >= bound" is "raw key >= a threshold" for each class; wave 0 finds the
+// thresholds, and those of +inf results (for the row's status), by search
+// over the keys of the non-NaN bf16 patterns.  A penalty that is not a
+// positive finite number breaks the monotony: such a row reports
+// FL_ROW_LIMIT.
 __global__ __launch_bounds__(LM_NT) void k_lm_thresh(const fl_lm_head_args a, LmWs ws) {
   constexpr int NW = LM_NT / WAVE;
   __shared__ uint4 keys[LM_NSAMPLE / 8];
@@ -578,58 +691,75 @@ __global__ __launch_bounds__(LM_NT) void k_lm_thresh(const fl_lm_head_args a, Lm
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid >> 6;
   if (tid == 0) {
     ws.cnt[b * LM_CNT_LD] = 0u;
-    ws.thr[b] = 0u;
     if (!ws.prep) ws.stat[b] = 0u;
   }
   const int K = a.top_k[b];
-  if (K < 1 || K > FL_LM_HEAD_MAX_TOPK) return;   // (the pick reports the row)
-  const int ns = ws.ns, nq = (ns + 7) >> 3;
-  const uint4* src = reinterpret_cast<const uint4*>(ws.skey + static_cast<size_t>(b) * ws.nsl);
-  for (int i = tid; i < nq; i += LM_NT) keys[i] = src[i];
-  int k = K;
-  uint32_t prefix = 0;   // high byte, once chosen
-  for (int pass = 0; pass < 2; ++pass) {
-    for (int i = tid; i < NW * 256; i += LM_NT) (&hist[0][0])[i] = 0u;
-    __syncthreads();   // (pass 0: also the keys)
-    for (int i = tid; i < nq; i += LM_NT) {
-      const uint4 q = keys[i];
-      const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-      const int nj = min(8, ns - 8 * i);
+  const bool topk = K >= 1 && K <= FL_LM_HEAD_MAX_TOPK;   // (else the pick reports the row)
+  uint32_t bound = 0;   // transformed key; 0: none
+  if (topk) {
+    const int ns = ws.ns, nq = (ns + 7) >> 3;
+    const uint4* src = reinterpret_cast<const uint4*>(ws.skey + static_cast<size_t>(b) * ws.nsl);
+    for (int i = tid; i < nq; i += LM_NT) keys[i] = src[i];
+    int k = K;
+    uint32_t prefix = 0;   // high byte, once chosen
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int i = tid; i < NW * 256; i += LM_NT) (&hist[0][0])[i] = 0u;
+      __syncthreads();   // (pass 0: also the keys)
+      for (int i = tid; i < nq; i += LM_NT) {
+        const uint4 q = keys[i];
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        const int nj = min(8, ns - 8 * i);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t key = (wd[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-        if (j < nj) {
-          if (pass == 0) atomicAdd(&hist[w][key >> 8], 1u);
-          else if ((key >> 8) == prefix) atomicAdd(&hist[w][key & 0xFFu], 1u);
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t key = (wd[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+          if (j < nj) {
+            if (pass == 0) atomicAdd(&hist[w][key >> 8], 1u);
+            else if ((key >> 8) == prefix) atomicAdd(&hist[w][key & 0xFFu], 1u);
+          }
         }
       }
-    }
-    __syncthreads();
-    if (w == 0) {
-      uint32_t c4[4], above = 0;
+      __syncthreads();
+      if (w == 0) {
+        uint32_t c4[4], above = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t c = 0;
+        for (int q = 0; q < 4; ++q) {
+          uint32_t c = 0;
 #pragma unroll
-        for (int v = 0; v < NW; ++v) c += hist[v][255 - 4 * lane - q];
-        c4[q] = c;
+          for (int v = 0; v < NW; ++v) c += hist[v][255 - 4 * lane - q];
+          c4[q] = c;
+        }
+        const int bin = wave_top_bin(c4, k, above);
+        if (lane == 0) {
+          s_bin = bin;
+          s_above = above;
+        }
       }
-      const int bin = wave_top_bin(c4, k, above);
-      if (lane == 0) {
-        s_bin = bin;
-        s_above = above;
-      }
-    }
-    __syncthreads();
-    const int bin = s_bin;
-    if (bin < 0) return;   // fewer than K keys: no bound (thr stays 0)
-    k -= static_cast<int>(s_above);
-    if (pass == 0) {
-      prefix = static_cast<uint32_t>(bin);
-    } else if (tid == 0) {
-      ws.thr[b] = (prefix << 8) | static_cast<uint32_t>(bin);
+      __syncthreads();
+      const int bin = s_bin;
+      if (bin < 0) break;   // fewer than K keys: no bound
+      k -= static_cast<int>(s_above);
+      if (pass == 0) prefix = static_cast<uint32_t>(bin);
+      else bound = (prefix << 8) | static_cast<uint32_t>(bin);
     }
   }
+  // wave v finds threshold v: candidates of non-members, of members, +inf
+  // of non-members, of members (a row without a penalty has no members)
+  static_assert(NW >= 4, "one wave per threshold");
+  if (w >= 4) return;
+  const float T = a.temperature[b], RT = T > 0.0f ? 1.0f / T : 0.0f, cap = a.softcap;
+  const bool pen = row_penalised(a, b);
+  const float RP = pen ? a.repetition_penalty[b] : 1.0f;
+  const bool bad = pen && !(RP > 0.0f && RP <= 3.402823466e38f);
+  if (w == 0 && bad && lane == 0) atomicOr(&ws.stat[b], static_cast<uint32_t>(FL_ROW_LIMIT));
+  const bool member = pen && (w & 1), inf = w >= 2;
+  uint32_t t = LM_KEY_NONE;   // (members of a row with a bad penalty: none, the row reports FL_ROW_LIMIT)
+  if ((inf || topk) && !(member && bad)) {
+    t = wave_first_key(LM_KEY_NINF, LM_KEY_PINF, [&](uint32_t r) {
+      const float y = lm_tval(bits_of_asc16(r), cap, member, RP, T, RT);
+      return inf ? y == __builtin_inff() : lm_key_of(y) >= bound;
+    });
+  }
+  if (lane == 0) ws.rthr[4 * static_cast<size_t>(b) + w] = t;
 }
 
 // ---------------------------------------------------------------- pick
@@ -685,8 +815,37 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick(const fl_lm_head_args a, LmWs
   }
   __syncthreads();
   if (status == 0) {
+    // each candidate's transformed key (the gemm kept its raw key)
+    const float T = a.temperature[b], RT = T > 0.0f ? 1.0f / T : 0.0f, cap = a.softcap;
+    const bool pen = row_penalised(a, b);
+    const float RP = pen ? a.repetition_penalty[b] : 1.0f;
+    const uint32_t* hb = ws.bits + static_cast<size_t>(b) * ws.bw;
     const uint64_t* cand = ws.cand + static_cast<size_t>(b) * LM_CAP;
-    for (uint32_t i = tid; i < nc; i += LM_NT) c[i] = cand[i];
+    constexpr int G = 4;   // candidates per thread and round: their loads go out together
+    for (uint32_t i0 = 0; i0 < nc; i0 += G * LM_NT) {
+      uint64_t v[G];
+      uint32_t hw[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t i = i0 + tid + g * LM_NT;
+        v[g] = i < nc ? cand[i] : 0ull;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t idx = ~static_cast<uint32_t>(v[g] & 0xFFFFFFFFull);
+        hw[g] = (pen && i0 + tid + g * LM_NT < nc) ? hb[idx >> 5] : 0u;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t i = i0 + tid + g * LM_NT;
+        if (i < nc) {
+          const uint32_t idx = ~static_cast<uint32_t>(v[g] & 0xFFFFFFFFull);
+          const bool member = (hw[g] >> (idx & 31)) & 1u;
+          const float y = lm_tval(bits_of_asc16(static_cast<uint32_t>(v[g] >> 32)), cap, member, RP, T, RT);
+          c[i] = (static_cast<uint64_t>(lm_key_of(y)) << 32) | (v[g] & 0xFFFFFFFFull);
+        }
+      }
+    }
     if (tid == 0) s_n = nc;
   }
   __syncthreads();
@@ -840,21 +999,16 @@ hipError_t launch_lm_head(const fl_lm_head_args& a, hipStream_t s) {
   if (ws.prep) hipLaunchKernelGGL(k_lm_prep, rows, dim3(LM_NT), 0, s, a, ws);
   const dim3 stiles(static_cast<unsigned>((ws.ns + 63) / 64));
   const dim3 tiles(static_cast<unsigned>((a.vocab + 255) / 256));
-  const bool sc = a.softcap > 0.0f;
   const int mb = static_cast<int>((a.batch + 15) / 16);
-  auto run = [&](auto tag_mb, auto tag_sc) {
+  auto run = [&](auto tag_mb) {
     constexpr int MB = decltype(tag_mb)::value;
-    constexpr bool SC = decltype(tag_sc)::value;
-    hipLaunchKernelGGL((k_lm_sample<MB, SC>), stiles, dim3(LM_NT), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_sample<MB>), stiles, dim3(LM_NT), 0, s, a, ws);
     hipLaunchKernelGGL(k_lm_thresh, rows, dim3(LM_NT), 0, s, a, ws);
-    hipLaunchKernelGGL((k_lm_gemm<MB, SC, LM_GW>), tiles, dim3(LM_GW * WAVE), 0, s, a, ws);
+    hipLaunchKernelGGL((k_lm_gemm<MB, LM_GW>), tiles, dim3(LM_GW * WAVE), 0, s, a, ws);
   };
-  using T1 = std::integral_constant<int, 1>;
-  using T2 = std::integral_constant<int, 2>;
-  using T4 = std::integral_constant<int, 4>;
-  if (mb <= 1) sc ? run(T1{}, std::true_type{}) : run(T1{}, std::false_type{});
-  else if (mb <= 2) sc ? run(T2{}, std::true_type{}) : run(T2{}, std::false_type{});
-  else sc ? run(T4{}, std::true_type{}) : run(T4{}, std::false_type{});
+  if (mb <= 1) run(std::integral_constant<int, 1>{});
+  else if (mb <= 2) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 4>{});
   hipLaunchKernelGGL(k_lm_pick, rows, dim3(LM_NT), 0, s, a, ws);
   return hipGetLastError();
 }

@@ -120,6 +120,48 @@ def test_rows_the_fused_path_cannot_decide():
     assert int(out.tokens[3]) < 6000
 
 
+def test_penalties_temperatures_and_overflow():
+    """The fused path compares raw logits against per-row thresholds that the
+    soft-cap, penalty and temperature map back from the bound; rows with a
+    penalty below 1 (raising negative and lowering positive values the other
+    way), tiny and zero temperatures, and a logit that overflows to +inf give
+    fl_sample's tokens, log-probabilities and status bits.  A penalty that is
+    not a positive finite number (rows 4 and 5) reports FL_ROW_LIMIT from the
+    fused path; lm_head_sample then uses fl_sample."""
+    B, D, V = 8, 256, 5000
+    print(f"[lm_head edges] B={B} D={D} V={V}", flush=True)
+    h, w = _operands(B, D, V, seed=21)
+    h[2] = 0
+    h[2, 0] = 2.0 ** 100
+    w[7, 0] = 2.0 ** 100          # row 2: logit 7 overflows to +inf, the others are about 2^96
+    g = torch.Generator().manual_seed(22)
+    kw = dict(temperature=torch.tensor([0.8, 0.01, 0.0, 1.3, 0.8, 0.8, 0.05, 2.0]),
+              top_k=torch.tensor([5, 20, 64, 1, 10, 10, 50, 33], dtype=torch.int32),
+              top_p=torch.tensor([0.9, 1.0, 0.7, 1.0, 0.9, 0.9, 0.95, 0.8]),
+              repetition_penalty=torch.tensor([0.7, 1.2, 0.5, 1.0, 0.0, -1.0, 1.5, 0.9]),
+              history=torch.randint(0, V, (B, 64), generator=g, dtype=torch.int32),
+              uniforms=torch.rand(B, generator=g))
+    kd = {k: v.cuda() for k, v in kw.items()}
+    plan = LmHeadPlan(h, w, return_logprobs=True, return_logits=True, **kd)
+    plan.launch()
+    torch.cuda.synchronize()
+    ref = sample_tokens(plan.logits, return_logprobs=True, check_status=False, **kd)
+    torch.cuda.synchronize()
+    st, rst = plan.status.tolist(), ref.status.tolist()
+    print(f"   fused status {st}, fl_sample status {rst}", flush=True)
+    L = _lib.FL_ROW_LIMIT
+    assert st[4] == L and st[5] == L
+    assert rst[2] & _lib.FL_ROW_INF and st[2] == rst[2]
+    for b in (0, 1, 3, 6, 7):
+        assert st[b] == rst[b] == 0, (b, st[b], rst[b])
+        assert int(plan.tokens[b]) == int(ref.tokens[b]), b
+        assert plan.logprob[b].view(torch.int32).item() == ref.logprobs[b].view(torch.int32).item(), b
+    out = lm_head_sample(h, w, return_logprobs=True, check_status=False, **kd)
+    torch.cuda.synchronize()
+    assert out.status.tolist()[:2] + out.status.tolist()[3:] == rst[:2] + rst[3:]
+    assert torch.equal(out.tokens[[0, 1, 3, 4, 5, 6, 7]], ref.tokens[[0, 1, 3, 4, 5, 6, 7]])
+
+
 def test_batches_above_64_rows_run_in_groups():
     B, D, V = 100, 256, 8192
     print(f"[lm_head groups] B={B}", flush=True)
