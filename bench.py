@@ -349,8 +349,9 @@ def bench_rowstats(args, dev) -> int:
 
 def bench_lmhead(args, dev) -> int:
     """The decode step's lm_head with the sampler in its epilogue
-    (lmhead_bf16_<B>x<D>x<V>): one step = LmHeadPlan.launch() (prep, sampled
-    bound, MFMA GEMM with the candidate epilogue, pick) for B rows of
+    (lmhead_bf16_<B>x<D>x<V>): one step = LmHeadPlan.launch() (history
+    bitmap, sampled gemm, bound and raw-key thresholds, MFMA GEMM with the
+    candidate epilogue, pick) for B rows of
     D-dimensional bf16 hidden states against a V x D bf16 weight, per-row
     top-k 1..64 with temperature, top-p, min-p and penalty.  Reported beside
     it: the unfused step (torch.matmul into [B, V] bf16 logits, then
@@ -412,7 +413,7 @@ def bench_lmhead(args, dev) -> int:
                      "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
                      "isolated_step_ms_p10": durs[len(durs) // 10],
                      "isolated_step_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": "k_lm_prep + k_lm_gemm<sample> + k_lm_thresh + k_lm_gemm + k_lm_pick",
+                     "kernel": "k_lm_prep + k_lm_sample + k_lm_thresh + k_lm_gemm + k_lm_pick",
                      "mfma_tflops": flops / (step_ms * 1e-3) / 1e12, "mfma_peak_tflops": 2500.0},
         "unfused": {"ms_per_step": unf_ms, "matmul_ms": gemm_ms,
                     "note": "torch.matmul(h, W.T) into [B, V] bf16 logits, then fl_sample (SamplerPlan)"},

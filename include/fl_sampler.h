@@ -282,18 +282,19 @@ int fl_row_stats(const fl_row_stats_args* args, void* stream);
  *
  *   logits[b, v] = bf16(sum_d hidden[b, d] * weight[v, d])   (fp32 accumulation)
  *
- * is computed on the matrix cores; each logit goes through soft-cap, the
- * repetition penalty (rows' history ids) and the temperature in the
- * epilogue, and only the values that can be among a row's top_k largest are
- * written (as candidates to the workspace), never the [batch, vocab] logits.
- * A second kernel samples each row from its candidates with fl_sample's
- * rules (top-k with ties, min-p, top-p, inverse-CDF or greedy selection,
+ * is computed on the matrix cores, and only the values that can be among a
+ * row's top_k largest after soft-cap, repetition penalty (rows' history ids)
+ * and temperature are written (as candidates to the workspace), never the
+ * [batch, vocab] logits.  A last kernel applies those transforms to the
+ * candidates and samples each row from them with fl_sample's rules (top-k
+ * with ties, min-p, top-p, inverse-CDF or greedy selection,
  * log-probability).  hidden [batch, dim] (row stride ld_hidden) and weight
  * [vocab, dim] (rows contiguous) are bf16; batch <= FL_LM_HEAD_MAX_BATCH, dim a
  * multiple of 64.  Per-row parameters as in fl_sample_args; top_k must lie in
- * 1 .. FL_LM_HEAD_MAX_TOPK.  A row whose top_k is outside that range, or whose
- * candidates exceed FL_LM_HEAD_MAX_CAND (more than that many values tie above
- * the threshold), reports FL_ROW_LIMIT and no token: sample it with fl_sample
+ * 1 .. FL_LM_HEAD_MAX_TOPK.  A row whose top_k is outside that range, whose
+ * repetition penalty is not a positive finite number, or whose candidates
+ * exceed FL_LM_HEAD_MAX_CAND (more than that many values tie above the
+ * threshold), reports FL_ROW_LIMIT and no token: sample it with fl_sample
  * over out_logits.  out_logits (NULL, or [batch, vocab] bf16) receives the
  * logits as computed, for such rows and for checks.  The workspace
  * (fl_lm_head_workspace_bytes) is the caller's scratch: calls that overlap in
