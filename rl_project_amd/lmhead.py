@@ -39,9 +39,11 @@ class LmHeadPlan:
     """A prepared fused lm_head + sampling step for ``hidden`` [B, D] bf16 and
     ``weight`` [V, D] bf16 (the lm_head weight; tied to the token embedding
     in the reference model).  Buffers and the argument block are built once;
-    ``launch()`` enqueues the three kernels with no allocation and no host
-    synchronisation, reading ``hidden``, the parameters and the uniforms at
-    launch time (a decode loop may overwrite them in place)."""
+    ``launch()`` enqueues the kernels (four, five with a penalty) on the
+    device's current stream with no allocation and no host synchronisation,
+    reading ``hidden``, the parameters and the uniforms at launch time (a
+    decode loop may overwrite them in place, or capture ``launch()`` in a
+    graph)."""
 
     def __init__(self, hidden: torch.Tensor, weight: torch.Tensor, *, temperature: PerRow = 1.0,
                  top_k: PerRow = 50, top_p: PerRow = None, min_p: PerRow = None,
@@ -96,12 +98,12 @@ class LmHeadPlan:
         self.args = a
         self._argp = ctypes.byref(a)
         self._fn = lib().fl_lm_head_sample
-        self._stream = _lib.stream_handle(dev)
+        self._dev = dev
         self.softcap = a.softcap
         self.history = history
 
     def launch(self) -> None:
-        rc = self._fn(self._argp, self._stream)
+        rc = self._fn(self._argp, _lib.stream_handle(self._dev))   # the current stream (graph capture records it)
         if rc:
             check(rc, "fl_lm_head_sample")
 

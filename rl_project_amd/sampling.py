@@ -185,7 +185,13 @@ class _Call:
         a.out_logprob, a.out_desc = ptr(self.logprob), ptr(self.desc)
         a.uniform_div = uniform_div
         self.args = a
-        self.stream = _lib.stream_handle(dev)
+        self.device = dev
+
+    @property
+    def stream(self) -> int:
+        """The device's current stream (read at each launch, as torch ops do:
+        a launch under graph capture is recorded into the graph)."""
+        return _lib.stream_handle(self.device)
 
     def run(self) -> "_Call":
         check(lib().fl_sample(ctypes.byref(self.args), self.stream), "fl_sample")
@@ -220,7 +226,10 @@ class SamplerPlan:
     built once, each ``launch()`` only enqueues the kernel (no allocation, no
     host synchronisation) -- for decode loops that resample the same buffers.
     Reads ``logits`` and the parameter tensors at launch time, so callers may
-    overwrite them in place between launches."""
+    overwrite them in place between launches.  Each launch goes to the
+    device's current stream, so a launch inside ``torch.cuda.graph`` capture
+    is recorded into the graph (the kernels allocate, copy and clear
+    nothing)."""
 
     def __init__(self, logits: torch.Tensor, exact_repeat: bool = False, **kw):
         want_logprob = kw.pop("return_logprobs", False)

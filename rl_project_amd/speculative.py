@@ -38,8 +38,9 @@ class SpecOutput:
 
 class SpecPlan:
     """A prepared ``speculative_verify``: arguments and outputs are built once;
-    each ``launch()`` enqueues the three kernels (target rows with the bonus
-    draw, draft rows, verify) with no allocation and no host synchronisation.
+    each ``launch()`` enqueues the kernels (target rows with the bonus draw,
+    draft rows, verify) on the device's current stream with no allocation and
+    no host synchronisation (so it may be captured in a graph).
     The logits, draft ids and uniforms are read at launch time, so a decode
     loop may overwrite them in place between launches.  ``sliced`` spreads the
     residual draw of each rejected sequence over several work-groups (with a
@@ -108,13 +109,13 @@ class SpecPlan:
         a.workspace_bytes = int(nbytes.value) if sliced else 0
         self._args = a
         self._argp = ctypes.byref(a)
-        self._stream = _lib.stream_handle(dev)
+        self._dev = dev
         self._verify = lib().fl_spec_verify_static if no_alloc else lib().fl_spec_verify
 
     def launch(self) -> None:
         self._t.run()
         self._d.run()
-        rc = self._verify(self._argp, self._stream)
+        rc = self._verify(self._argp, _lib.stream_handle(self._dev))   # the current stream (graph capture records it)
         if rc:
             check(rc, self._verify.__name__)
 
