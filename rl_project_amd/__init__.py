@@ -4,10 +4,17 @@ Public API
 ----------
 apply_sampling_filters, sample_from_logits, generate_tokens
     Reference-compatible functions (src/forgeline/models/generation/sampling.py).
-sample_tokens, describe_rows, filtered_outputs
-    Batched entry points with heterogeneous per-row parameters.
-speculative_verify, SpeculativeGenerator
-    Speculative-decoding accept / resample (models/generation/speculative.py).
+sample_tokens, describe_rows, filtered_outputs, SamplerPlan
+    Batched entry points with heterogeneous per-row parameters (SamplerPlan:
+    prepared once, one launch per decode step, capturable in a graph).
+BatchedSampler
+    A decode group's sampling state on the device (inference/engine.py:114-139).
+speculative_verify, SpecPlan, SpeculativeGenerator, MTPSpeculativeGenerator
+    Speculative-decoding accept / resample and the generators over B sequences
+    (models/generation/speculative.py).
+lm_head_sample, LmHeadPlan
+    lm_head and sampling in one call, without the [B, V] logits
+    (models/transformer/model.py:190, :201).
 token_logprobs_from_logits, entropy_from_logits, kl_full_distribution, row_stats
     Full-distribution log-prob / entropy / KL in one pass (models/policy.py,
     training/common/logprobs.py).
@@ -16,8 +23,8 @@ SamplingParams
 """
 
 from .params import GenerationSettings, SamplingParams, SamplingParamsError
-from .sampling import (SampleOutput, SamplingError, apply_sampling_filters, describe_rows, filtered_outputs,
-                       generate_tokens, sample_from_logits, sample_tokens)
+from .sampling import (SampleOutput, SamplerPlan, SamplingError, apply_sampling_filters, describe_rows,
+                       filtered_outputs, generate_tokens, sample_from_logits, sample_tokens)
 from .speculative import MTPSpeculativeGenerator, SpeculativeGenerator, SpecOutput, SpecPlan, speculative_verify
 from .engine import BatchedSampler
 from .logprobs import RowStats, entropy_from_logits, kl_full_distribution, row_stats, token_logprobs_from_logits
@@ -25,7 +32,7 @@ from .lmhead import LmHeadOutput, LmHeadPlan, lm_head_sample
 
 __all__ = [
     "apply_sampling_filters", "sample_from_logits", "generate_tokens",
-    "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplingError",
+    "sample_tokens", "describe_rows", "filtered_outputs", "SampleOutput", "SamplerPlan", "SamplingError",
     "speculative_verify", "SpeculativeGenerator", "MTPSpeculativeGenerator", "SpecOutput", "SpecPlan",
     "BatchedSampler", "row_stats", "RowStats", "token_logprobs_from_logits", "entropy_from_logits", "kl_full_distribution",
     "SamplingParams", "GenerationSettings", "SamplingParamsError",
