@@ -632,19 +632,9 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
       if (!(1.0f >= R.MP)) {
         st |= FL_ROW_ALL_MASKED;  // min_p > 1 removes every value
       } else {
-        // smallest key whose value passes exp(y - M) >= min_p (kmx passes)
-        auto pass = [&](uint32_t k) { return expf(f32_of_key(k) - M) >= R.MP; };
-        uint32_t lo = KEY_MIN_FINITE, hi = kmx;
-        if (pass(lo)) {
-          kp = lo;
-        } else {
-          while (hi - lo > 1u) {
-            const uint32_t mid = lo + (hi - lo) / 2u;
-            if (pass(mid)) hi = mid;
-            else lo = mid;
-          }
-          kp = hi;
-        }
+        // smallest key whose value passes exp(y - M) >= min_p (kmx passes): a
+        // 64-way search of the wave over the monotone predicate
+        kp = wave_first_key(KEY_MIN_FINITE, kmx, [&](uint32_t k) { return expf(f32_of_key(k) - M) >= R.MP; });
         bm = fbin(f32_of_key(kp), c);
       }
     }
@@ -794,14 +784,31 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
         const bool hist = w >= 2 * nr;
         const bool upper = w & 1;
         auto bin_of_x = [&](uint32_t kx) { return fbin(X.y(f32_of_key(kx), hist), c); };
+        auto pred = [&](uint32_t kx) { return upper ? bin_of_x(kx) < rl[r] : bin_of_x(kx) <= rh[r]; };
         // finite x only: +-inf map to +-inf (a non-finite y is never gathered)
         const uint32_t k0 = f32_key(-FLT_MAX), k1 = f32_key(FLT_MAX) + 1u;
-        uint32_t k;
-        if (!upper) {
-          k = wave_first_key(k0, k1, [&](uint32_t kx) { return bin_of_x(kx) <= rh[r]; });
-        } else {
-          k = wave_first_key(k0, k1, [&](uint32_t kx) { return bin_of_x(kx) < rl[r]; });
+        // First a window of 2^13 keys around an approximate inverse of the
+        // bin bound (temperature, penalty and soft-cap undone); if the
+        // predicate does not change inside it (checked at its two ends), the
+        // whole range.  Either way the result is the first key where the
+        // monotone predicate holds.
+        constexpr uint32_t HALF = 4096;
+        float xa = upper ? fub(rl[r], c) : fub(rh[r] + 1, c);
+        if (X.t > 0.0f) xa *= X.t;
+        if (hist) xa = xa > 0.0f ? xa * X.rp : xa / X.rp;
+        if (X.cap > 0.0f) xa = fabsf(xa) < X.cap ? atanhf(xa / X.cap) * X.cap : __builtin_nanf("");
+        uint32_t k = k1;
+        bool found = false;
+        if (fabsf(xa) <= FLT_MAX) {   // (false for NaN)
+          const uint32_t ka = f32_key(xa);
+          const uint32_t a0 = ka > k0 + HALF ? ka - HALF : k0;
+          const uint32_t b0 = ka + HALF < k1 ? ka + HALF : k1;
+          if ((a0 == k0 || !pred(a0 - 1u)) && pred(b0 - 1u)) {
+            k = wave_first_key(a0, b0, pred);
+            found = true;
+          }
         }
+        if (!found) k = wave_first_key(k0, k1, pred);
         if (lane == 0) {
           // empty interval: lower end +inf or upper end -inf
           if (!upper) sh.xlo[hist][r] = k == k1 ? __builtin_inff() : f32_of_key(k);
