@@ -497,9 +497,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
   FL_MARK(12);
   // ------------------------------------------------ repetition penalty
   // each unique id moves one count from its pattern to its penalised pattern
-  auto penalise = [&](uint32_t raw) {
-    const uint32_t z = elem_bits(raw);
-    const uint32_t zp = penalised_bits<D>(z, RP);
+  auto move = [&](uint32_t raw, uint32_t z, uint32_t zp) {
     if (zp != z) {
       // (a soft-capped raw -inf was counted in this lane's -inf counter)
       if (SC && raw == NEG_INF_RAW) atomicAdd(&sh.hist[inf_word], 0xFFFFFFFFu);
@@ -507,9 +505,22 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       atomicAdd(&sh.hist[zp >> 1], (zp & 1u) ? 0x10000u : 1u);
     }
   };
+  auto penalise = [&](uint32_t raw) {
+    const uint32_t z = elem_bits(raw);
+    move(raw, z, penalised_bits<D>(z, RP));
+  };
+  // the patterns of the owned prefetched ids, kept for the identification
+  // (16 bits each, in one VGPR)
+  static_assert(HPRE == 2, "two patterns per word");
+  uint32_t hz = 0;
 #pragma unroll
-  for (int k = 0; k < HPRE; ++k)
-    if (own[k]) penalise(xh[k]);
+  for (int k = 0; k < HPRE; ++k) {
+    if (own[k]) {
+      const uint32_t z = elem_bits(xh[k]);
+      hz |= z << (16 * k);
+      move(xh[k], z, penalised_bits<D>(z, RP));
+    }
+  }
   if (!wide) {
     for (int i = tid + ((hist_rows && !HEAVY) ? HPRE * NT : 0); i < H; i += NT) {
       const int id = hid[i];
@@ -992,16 +1003,6 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       else if constexpr (!HEAVY) r[j] = d[j];
       else r[j] = make_uint4(0, 0, 0, 0);
     }
-    // the logits of this thread's first HPRE history ids again (keeping them
-    // in VGPRs since the count pass would spill them), issued now so that the
-    // loads overlap the member counting
-    // (a buffer load by 32-bit offset: nothing 64-bit to keep from the first
-    // read of these logits)
-    const __amdgpu_buffer_rsrc_t rall = row_rsrc(row, 2u * static_cast<uint32_t>(V));
-    uint32_t xh2[HPRE];
-#pragma unroll
-    for (int k = 0; k < HPRE; ++k)
-      xh2[k] = __builtin_amdgcn_raw_buffer_load_b16(rall, own[k] ? 2 * hpre[k] : 0, 0, 0);
     lds_barrier();  // the decisions are in sh.dec; the entries may be overwritten
     FL_MARK(13);
     y_sel = sh.dec.y_sel;
@@ -1156,9 +1157,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
     FL_MARK(14);
     // history elements whose penalised value lies in a target group
     if (pen) {
-      auto hist_candidate = [&](int id, uint32_t raw) {
-        const uint32_t z = elem_bits(raw);
-        const uint32_t zp = penalised_bits<D>(z, RP);
+      auto hist_candidate = [&](int id, uint32_t z, uint32_t zp) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           if (!active[t]) continue;
@@ -1171,14 +1170,19 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       };
 #pragma unroll
       for (int k = 0; k < HPRE; ++k)
-        if (own[k]) hist_candidate(hpre[k], xh2[k]);
+        if (own[k]) {
+          const uint32_t z = (hz >> (16 * k)) & 0xFFFFu;
+          hist_candidate(hpre[k], z, penalised_bits<D>(z, RP));
+        }
       // (wide rows claimed every id in the windowed pass: none was prefetched)
       for (int i = tid + ((hist_rows && !wide && !HEAVY) ? HPRE * NT : 0); i < H; i += NT) {
         if (!((sh.owner[i >> 5] >> (i & 31)) & 1u)) continue;
         const int id = hid[i];
-        hist_candidate(id, row[id]);
+        const uint32_t z = elem_bits(row[id]);
+        hist_candidate(id, z, penalised_bits<D>(z, RP));
       }
     }
+    FL_MARK(10);
     __syncthreads();
     FL_MARK(7);
 #pragma unroll
