@@ -84,6 +84,7 @@ constexpr float ANCHOR_UP = 24.0f;         // bin 0 starts this far above the an
 constexpr int CNT_SH = 45;                 // bin word: count << 45 | sum of 2^-26 terms
 constexpr uint64_t TERM_MASK = (1ull << CNT_SH) - 1u;
 constexpr int NRANGE = 4;                  // bin ranges gathered by the second read
+constexpr int RANK_SORT_MAX = 384;         // candidates sorted by rank counting; more by the bitonic network
 
 // e in [0, 1] as fixed point round(e * 2^45) (halves rounded up).
 __device__ __forceinline__ uint64_t fx45(float e) {
@@ -272,16 +273,64 @@ __device__ __forceinline__ void wave_append(bool p, uint64_t v, uint32_t* counte
   if (p && base + below < static_cast<uint32_t>(CAP)) buf[base + below] = v;
 }
 
-// Descending bitonic sort of buf[0, n) in LDS (n <= CAP); pads with zeros.
+// Compare-exchange of one entry v (index idx) with the entry j positions
+// away, held by lane ^ j (j <= 32), in the bitonic step (k, j): the lower
+// index keeps the larger value where the k-block runs descending.
+__device__ __forceinline__ uint64_t bitonic_lane_step(uint64_t v, int idx, int k, int j) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), j, WAVE);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), j, WAVE);
+  const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
+  const bool keep_max = ((idx & j) == 0) == ((idx & k) == 0);
+  return keep_max ? (v > pv ? v : pv) : (v < pv ? v : pv);
+}
+
+// Steps (k, j) for j = jtop .. 1 (jtop <= 64) on one 128-entry block held in
+// registers: lane l holds entries base + l (v0) and base + 64 + l (v1).
+__device__ __forceinline__ void bitonic_block_steps(uint64_t& v0, uint64_t& v1, int base, int k, int jtop) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int i0 = base + lane, i1 = i0 + WAVE;
+  for (int j = jtop; j > 0; j >>= 1) {
+    if (j == WAVE) {  // the pair (base + l, base + 64 + l) lies in one lane
+      const bool desc = (i0 & k) == 0;
+      const uint64_t mx = v0 > v1 ? v0 : v1, mn = v0 > v1 ? v1 : v0;
+      v0 = desc ? mx : mn;
+      v1 = desc ? mn : mx;
+    } else {
+      v0 = bitonic_lane_step(v0, i0, k, j);
+      v1 = bitonic_lane_step(v1, i1, k, j);
+    }
+  }
+}
+
+// Descending bitonic sort of buf[0, n) in LDS (n <= CAP); pads with zeros to
+// a power of two P >= 128.  The steps of distance j <= 64 act within blocks
+// of 128 entries: each wave loads a block into registers (two entries per
+// lane), runs all such steps of one k there (lane exchanges by shuffles),
+// and stores it back -- one LDS round trip where the network would take one
+// per step.  Blocks of k <= 128 are sorted whole in one such pass.  Steps of
+// distance >= 128 go through LDS, one pair per thread, between block
+// barriers.
 __device__ void bitonic_desc(uint64_t* buf, int n) {
-  int P = 2;
+  int P = 128;
   while (P < n) P <<= 1;
   for (int i = n + threadIdx.x; i < P; i += NT) buf[i] = 0;
   __syncthreads();
-  for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = threadIdx.x / WAVE;
+  const int nblk = P / (2 * WAVE);
+  // blocks sorted whole: k = 2 .. 128
+  for (int blk = wave; blk < nblk; blk += NWAVE) {
+    const int base = blk * 2 * WAVE;
+    uint64_t v0 = buf[base + lane], v1 = buf[base + WAVE + lane];
+    for (int k = 2; k <= 2 * WAVE; k <<= 1) bitonic_block_steps(v0, v1, base, k, k >> 1);
+    buf[base + lane] = v0;
+    buf[base + WAVE + lane] = v1;
+  }
+  for (int k = 4 * WAVE; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > WAVE; j >>= 1) {
+      __syncthreads();
       for (int i = threadIdx.x; i < (P >> 1); i += NT) {
-        const int a = 2 * j * (i / j) + (i % j);
+        const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1));  // 2 j (i / j) + i % j (j a power of 2)
         const int c = a + j;
         const uint64_t x = buf[a], y = buf[c];
         const bool desc = (a & k) == 0;
@@ -290,9 +339,17 @@ __device__ void bitonic_desc(uint64_t* buf, int n) {
           buf[c] = x;
         }
       }
-      __syncthreads();
+    }
+    __syncthreads();
+    for (int blk = wave; blk < nblk; blk += NWAVE) {
+      const int base = blk * 2 * WAVE;
+      uint64_t v0 = buf[base + lane], v1 = buf[base + WAVE + lane];
+      bitonic_block_steps(v0, v1, base, k, WAVE);
+      buf[base + lane] = v0;
+      buf[base + WAVE + lane] = v1;
     }
   }
+  __syncthreads();
 }
 
 // Descending order of buf[0, n), n <= NT, whose nonzero entries are distinct
@@ -859,10 +916,14 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
       nm += mem ? 1u : 0u;
       sh.cand[i] = mem ? (static_cast<uint64_t>(f32_key(y)) << 32) | (v & 0xFFFFFFFFull) : 0ull;
     }
+    FL_MARK(10);
     nm = block_reduce<uint32_t>(nm, OpAdd(), sh.redu);
     if (nm != static_cast<uint32_t>(ngath)) return false;
+    FL_MARK(11);
     // members first (every member word is nonzero)
-    if (ns <= NT) rank_sort_desc(sh.cand, sh.cscan, ns);
+    // (the rank sort's work grows as ns^2 / 16 cycles: 1.7 us at 256,
+    // 27 us at 1024; the bitonic network's as its steps)
+    if (ns <= RANK_SORT_MAX) rank_sort_desc(sh.cand, sh.cscan, ns);
     else bitonic_desc(sh.cand, ns);
     FL_MARK(6);
     const int n = ngath;
