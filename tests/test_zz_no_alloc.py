@@ -46,7 +46,7 @@ def _static_call(plan):
     t = torch.full_like(plan.tokens, -7)
     r = torch.full_like(plan.ratio, -7.0)
     a.out_n_accepted, a.out_tokens, a.out_ratio = n.data_ptr(), t.data_ptr(), r.data_ptr()
-    rc = _lib.lib().fl_spec_verify_static(ctypes.byref(a), plan._stream)
+    rc = _lib.lib().fl_spec_verify_static(ctypes.byref(a), _lib.stream_handle(plan._dev))
     assert rc == _lib.FL_OK, _lib.lib().fl_last_error().decode()
     return n, t, r
 
