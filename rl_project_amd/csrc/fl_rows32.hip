@@ -179,6 +179,41 @@ struct Xform {
     if (TDIV) z = div_rt(z, t, rt);
     return z + 0.0f;
   }
+  // yt of the four elements of a chunk (history bits hb).  With TDIV the
+  // range guard of div_rt is taken once for the chunk: when every element
+  // passes it (the usual case) each quotient is Markstein's two FMAs, else
+  // each element takes div_rt.  Equal to yt() bit for bit.
+  template <bool TDIV, bool PEN>
+  __device__ __forceinline__ void yt4(const float (&xs)[4], uint32_t hb, float (&y)[4]) const {
+    if constexpr (!TDIV) {  // (element by element: soft-capped rows interleave better)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = yt<false, PEN>(xs[e], (hb >> e) & 1u);
+      return;
+    }
+    float z[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      z[e] = xs[e];
+      if (cap > 0.0f) z[e] = softcap_val<F32>(z[e], cap);
+      if (PEN && ((hb >> e) & 1u)) z[e] = penalty_val<F32>(z[e], rp);
+    }
+    if constexpr (TDIV) {
+      float q0[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q0[e] = z[e] * rt;
+      // (NaN: fminf / fmaxf skip it and the FMAs return NaN, as the division does)
+      const float zmin = fminf(fminf(fabsf(z[0]), fabsf(z[1])), fminf(fabsf(z[2]), fabsf(z[3])));
+      const float qmin = fminf(fminf(fabsf(q0[0]), fabsf(q0[1])), fminf(fabsf(q0[2]), fabsf(q0[3])));
+      const float qmax = fmaxf(fmaxf(fabsf(q0[0]), fabsf(q0[1])), fmaxf(fabsf(q0[2]), fabsf(q0[3])));
+      if (zmin >= 0x1p-100f && qmin >= 0x1p-100f && qmax <= 0x1p100f) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(__builtin_fmaf(-t, q0[e], z[e]), rt, q0[e]) + 0.0f;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = div_rt(z[e], t, rt) + 0.0f;
+      }
+    }
+  }
   // history bits of elements 4c .. 4c+3
   __device__ __forceinline__ uint32_t nibble(int c) const {
     return (pen && c < nch) ? (hbits[c >> 3] >> ((c & 7) * 4)) & 0xFu : 0u;
@@ -528,8 +563,10 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
       const int ch = u * NT + tid;
       const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+      float y4[4];
+      X.yt4<TDIV, PEN>(xs, hb, y4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) yb[4 * u + e] = X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u);
+      for (int e = 0; e < 4; ++e) yb[4 * u + e] = y4[e];
     }
   }
 #pragma unroll
@@ -593,8 +630,7 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
       const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
       float y4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y4[e] = X.yt<TDIV, PEN>(xs[e], (hb >> e) & 1u);
+      X.yt4<TDIV, PEN>(xs, hb, y4);
       add4(ch, y4);
       __builtin_amdgcn_sched_barrier(0);
     }
