@@ -2,8 +2,8 @@
 vocabularies of 1, 2, 3, 8 and 65 values in every dtype, with top-k above
 and at the vocabulary, min-p, top-p, penalties below and above 1 and greedy
 rows; logits given as a strided view (rows of a wider buffer), which must
-sample like their contiguous copy; and a soft-cap whose x / cap spans both
-branches of the kernels' tanh."""
+sample like their contiguous copy; a soft-cap whose x / cap spans both
+branches of the kernels' tanh; and float32 rows saturated by the soft-cap."""
 
 import pytest
 import torch
@@ -99,3 +99,30 @@ def test_softcap_on_both_sides_of_the_polynomial_range(dtype):
     err = float(((got - ref).abs() / ulp).max())
     print(f"   max |filtered - oracle| = {err:.2f} ulp", flush=True)
     assert err <= (4 if dtype == torch.float32 else 2)
+
+
+def test_float32_rows_saturated_by_the_softcap():
+    """Float32 logits far beyond the soft-cap (x ~ N(0, 150^2), cap 10): most
+    values sit within an ulp or two of +-cap, where tanh is flat.  The first
+    read's bins then hold long runs of equal values, and the raw-logit
+    interval of a bin range is far from the inverse of its bounds (atanh is
+    ill-conditioned there), so the interval searches fall back from their
+    window to the whole key range.  Tokens classify against the oracle."""
+    B, V, cap = 6, 50000, 10.0
+    print(f"[edges saturated softcap] B={B} V={V} cap={cap}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    x = 150.0 * torch.randn(B, V, generator=g)
+    T = torch.tensor([1.0, 0.8, 1.5, 1.0, 0.5, 1.0])
+    K = torch.tensor([0, 0, 0, 100, 0, 5], dtype=torch.int32)
+    P = torch.tensor([0.9, 0.5, 0.99, 1.0, 0.7, 1.0])
+    MP = torch.tensor([0.0, 0.0, 0.0, 0.1, 0.0, 0.0])
+    RP = torch.ones(B)
+    U = torch.rand(B, generator=g)
+    w = workloads.SampleWorkload("edges_saturated", x, T, K, P, MP, RP, None, None, U, softcap=cap)
+    wd = w.to("cuda")
+    out = sample_tokens(wd.logits, **wd.kwargs())
+    torch.cuda.synchronize()
+    assert out.status.tolist() == [0] * B
+    summ, verdicts = classify_workload(w, out.tokens.cpu())
+    print(f"   {summ}", flush=True)
+    assert summ["MISMATCH"] == 0, [(b, v.details) for b, v in enumerate(verdicts) if not v.ok][:4]
