@@ -24,6 +24,11 @@ oracle's, except for
                             (``selection_near``); greedy picks must be able to
                             win the first-index argmax under ``RK``
                             (``greedy_near``);
+                 speculative  accept ratios and residual / bonus draws
+                            with the oracle's filtered rows and, where a
+                            row's top-p cut is open (``_top_p_count_range``),
+                            with each other allowed kept count
+                            (``_top_p_alternatives``);
                the distance from the boundary is reported;
   * CONSEQ  -- a token difference that follows from an explained mask
                difference (the candidate's token is what the selection rule
@@ -31,7 +36,8 @@ oracle's, except for
 Anything else is MISMATCH.  ``tests/test_classify.py`` plants mistakes
 (an extra token, a top-p cut moved by one value group, a token one position
 off in the inverse CDF, a wrong greedy tie-break, wrong accept / residual /
-bonus draws) and requires MISMATCH for each.
+bonus draws, tokens next to a bonus draw at an open top-p cut) and requires
+MISMATCH for each.
 
 Decision predicates re-evaluated here (reference ``sampling.py:36-61``):
 top-k keeps y >= k-th largest; min-p keeps round(e r) >= round(round(r) min_p)
@@ -359,13 +365,52 @@ def _interval_ok(c: np.ndarray, d: np.ndarray, j: int, t: float) -> tuple:
     return bool(lo - dlo <= t < hi + dhi), max(0.0, lo - t, t - hi)
 
 
+def _top_p_alternatives(row: torch.Tensor, p: O.RowParams, softcap: float = 0.0, cap_per_group: int = 16) -> list:
+    """Filtered rows (dtype, [V]) whose kept sets differ from the oracle's
+    only in the kept count of a top-p boundary value group, for every count
+    the rounding doubt of the cumulative sums allows (``_top_p_count_range``):
+    the group of the smallest kept value and the group of the largest value
+    that top-p removed.  Members of a group are kept lowest index first, as
+    the kernels keep them.  Empty when top-p is off or its cut is certain."""
+    if p.top_p is None or not (0.0 < p.top_p < 1.0):
+        return []
+    dt = row.dtype
+    y_t = O.pre_filter_values(row[None], p.temperature, 1.0, None, softcap)[0]
+    y = y_t.double().numpy()
+    stage = O._top_k(y_t[None].clone(), p.top_k or None)
+    stage = O._min_p(stage, p.min_p or None)
+    surv = ~np.isneginf(stage[0].double().numpy())
+    _, filt = O.filtered_probs(row, p, softcap)
+    keep = ~np.isneginf(filt.double().numpy())
+    groups = []
+    if keep.any():
+        groups.append(float(y[keep].min()))
+    if (surv & ~keep).any():
+        groups.append(float(y[surv & ~keep].max()))
+    alts = []
+    for v in groups:
+        grp = np.nonzero(y == v)[0]
+        lo_n, hi_n, _ = _top_p_count_range(y, surv, grp, p.top_p, dt)
+        cur = int(keep[grp].sum())
+        for c in range(lo_n, min(hi_n, lo_n + cap_per_group) + 1):
+            if c == cur:
+                continue
+            k2 = keep.copy()
+            k2[grp] = False
+            k2[grp[:c]] = True
+            alts.append(torch.from_numpy(np.where(k2, y, -np.inf)).to(dt))
+    return alts
+
+
 def classify_spec(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, p: O.RowParams,
                   u_accept: torch.Tensor, u_resample: torch.Tensor, got_n, got_tokens, softcap: float = 0.0,
                   ref: Optional[List[O.SpecResult]] = None):
     """Per sequence: EXACT, NEAR (the first difference is an accept decision
     whose ``u`` lies within the doubt of the ratio, or a resampled / bonus
     token whose cumulative interval lies within the doubt of the draw) or
-    MISMATCH.  Returns (summary, [(kind, distance)], oracle results)."""
+    MISMATCH.  Where a row's top-p cut is itself open under rounding, the
+    filtered rows with the other allowed kept counts (``_top_p_alternatives``)
+    are tried too.  Returns (summary, [(kind, distance)], oracle results)."""
     if ref is None:
         ref = O.speculative_verify(target, draft, draft_ids, p, u_accept, u_resample, softcap=softcap)
     B, K = draft_ids.shape
@@ -390,6 +435,22 @@ def classify_spec(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
             p64 = float(torch.softmax(ft.double(), -1)[d])
             q64 = float(torch.softmax(fd.double(), -1)[d])
             ok, dist = _accept_window(p64, q64, r.accept_ratio[m], float(u_accept[b, m]), pt.dtype)
+            if not ok:
+                for at in [ft] + _top_p_alternatives(target[b, m], p, softcap):
+                    for ad in [fd] + _top_p_alternatives(draft[b, m], p, softcap):
+                        if at is ft and ad is fd:
+                            continue
+                        pa = torch.softmax(at, -1)
+                        qa = torch.softmax(ad, -1)
+                        ra = _ratio(float(pa[d]), float(qa[d]), pt.dtype)
+                        ok2, d2 = _accept_window(float(torch.softmax(at.double(), -1)[d]),
+                                                 float(torch.softmax(ad.double(), -1)[d]), ra,
+                                                 float(u_accept[b, m]), pt.dtype)
+                        if ok2:
+                            ok, dist = True, d2
+                            break
+                    if ok:
+                        break
             out.append(("NEAR" if ok else "MISMATCH", dist))
             continue
         t = float(np.float64(np.float32(u_resample[b])))
@@ -401,9 +462,27 @@ def classify_spec(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
             q64 = torch.softmax(fd.double(), -1).numpy()
             c, dd = _residual_doubt(pt, pd, p64, q64)
             ok, dist = _interval_ok(c, dd, g, t) if 0 <= g < c.size else (False, float("inf"))
+            if not ok:
+                for at in [ft] + _top_p_alternatives(target[b, n], p, softcap):
+                    for ad in [fd] + _top_p_alternatives(draft[b, n], p, softcap):
+                        if at is ft and ad is fd:
+                            continue
+                        ca, da = _residual_doubt(torch.softmax(at, -1), torch.softmax(ad, -1),
+                                                 torch.softmax(at.double(), -1).numpy(),
+                                                 torch.softmax(ad.double(), -1).numpy())
+                        if 0 <= g < ca.size and _interval_ok(ca, da, g, t)[0]:
+                            ok, dist = True, 0.0
+                            break
+                    if ok:
+                        break
         else:       # bonus from target position K
             _, ft = O.filtered_probs(target[b, K], p, softcap)
             ok, dist = selection_near(ft, float(u_resample[b]), g)
+            if not ok:
+                for at in _top_p_alternatives(target[b, K], p, softcap):
+                    if selection_near(at, float(u_resample[b]), g)[0]:
+                        ok, dist = True, 0.0
+                        break
         out.append(("NEAR" if ok else "MISMATCH", dist))
     kinds = [k for k, _ in out]
     summ = {k: kinds.count(k) for k in ("EXACT", "NEAR", "MISMATCH")}
