@@ -4,8 +4,10 @@ distributions (normal, coarse grid with heavy ties, wide, masked, one
 dominant value), every filter, penalties above and below 1, ragged
 histories and soft-caps.  Every row must be EXACT, TIE or NEAR to the oracle,
 its filtered values equal the oracle's, and its probabilities lie within
-1e-6 (float32) / 1e-2 (16-bit) of the exact softmax of its filtered logits."""
+1e-6 (float32) / 1e-2 (16-bit) of the exact softmax of its filtered logits.
+Speculative cases include sequences whose draws meet an open top-p cut."""
 
+import dataclasses
 import random
 
 import pytest
@@ -102,3 +104,29 @@ def test_random_speculative_cases():
         for k, v in summ.items():
             counts[k] = counts.get(k, 0) + v
     print(counts)
+
+
+# (seed, sequence) of a longer speculative sweep whose residual or bonus draw
+# meets a row with an open top-p cut (the exclusive mass within ~3e-7 of
+# top-p): the kernel's token must be one that an allowed kept count gives
+OPEN_CUT_CASES = [(5062, 8), (5083, 28), (5085, 15), (5088, 37), (5101, 40), (5165, 6)]
+
+
+def test_speculative_draws_at_open_top_p_cuts():
+    for seed, b in OPEN_CUT_CASES:
+        rng = random.Random(seed)
+        B, V, K = rng.choice([1, 3, 8, 32, 64]), rng.choice([100, 4096, 32000, 128256]), rng.choice([1, 2, 5])
+        T, P = rng.choice([0.5, 0.8, 1.0]), rng.choice([0.9, 0.95, 1.0])
+        print(f"[open top-p cut] seed={seed} B={B} V={V} K={K} T={T} P={P} sequence {b}", flush=True)
+        w = workloads.make_spec(seed=seed, batch=B, vocab=V, k=K, draft_sampler=oracle_draft_sampler(T, P))
+        w.temperature, w.top_p = T, P
+        w.draft_ids = oracle_draft_sampler(T, P)(w.draft.reshape(-1, V), w.extra["u_draft"]).view(B, K)
+        d = w.to("cuda")
+        out = speculative_verify(d.target, d.draft, d.draft_ids, temperature=T, top_p=P, u_accept=d.u_accept,
+                                 u_resample=d.u_resample)
+        torch.cuda.synchronize()
+        ws = dataclasses.replace(w, target=w.target[b:b + 1], draft=w.draft[b:b + 1], draft_ids=w.draft_ids[b:b + 1],
+                                 u_accept=w.u_accept[b:b + 1], u_resample=w.u_resample[b:b + 1])
+        summ, verdicts, _ = classify_spec(ws, out.n_accepted[b:b + 1], out.tokens[b:b + 1])
+        print(f"   {verdicts}", flush=True)
+        assert summ["MISMATCH"] == 0, (seed, b, verdicts)
