@@ -9,7 +9,12 @@
   inverse-CDF convention) classifies every row EXACT or NEAR.
 * Rows the fused path leaves at FL_ROW_LIMIT (top-k off or above 64, more
   than 4096 values tied above the threshold) are sampled by ``fl_sample``
-  through ``lm_head_sample``."""
+  through ``lm_head_sample``.
+* Seeded random cases (batch 1 to 70, dim 64 to 4096, vocabularies of 100 to
+  128256, soft-caps, per-row parameters and ragged history lengths): tokens
+  and log-probabilities bit-equal to ``fl_sample`` on the GEMM's logits."""
+
+import random
 
 import pytest
 import torch
@@ -173,6 +178,33 @@ def test_batches_above_64_rows_run_in_groups():
     torch.cuda.synchronize()
     assert torch.equal(out.tokens, ref.tokens)
     _check_logits(h, w, out.logits)
+
+
+@pytest.mark.parametrize("first", [0, 12])
+def test_random_lm_head_cases(first):
+    for seed in range(first, first + 12):
+        rng = random.Random(1000 + seed)
+        B = rng.choice([1, 3, 16, 17, 40, 64, 70])
+        D = rng.choice([64, 256, 1024, 4096])
+        V = rng.choice([100, 4099, 32000, 50257, 128256])
+        cap = rng.choice([0.0, 0.0, 30.0, 5.0])
+        print(f"[lm_head random] seed={1000 + seed} B={B} D={D} V={V} softcap={cap}", flush=True)
+        h, w = _operands(B, D, V, seed=1000 + seed, scale=rng.choice([1.0, 2.5, 8.0]))
+        g = torch.Generator().manual_seed(2000 + seed)
+        kw = dict(temperature=torch.tensor([rng.choice([0.0, 0.3, 0.8, 1.0, 1.5]) for _ in range(B)]),
+                  top_k=torch.tensor([rng.choice([1, 2, 10, 50, 64]) for _ in range(B)], dtype=torch.int32),
+                  top_p=torch.tensor([rng.choice([1.0, 0.5, 0.9, 0.99]) for _ in range(B)]),
+                  min_p=torch.tensor([rng.choice([0.0, 0.0, 0.05, 0.3]) for _ in range(B)]),
+                  repetition_penalty=torch.tensor([rng.choice([1.0, 1.3, 0.8]) for _ in range(B)]),
+                  history=torch.randint(0, V, (B, rng.choice([1, 32, 300])), generator=g, dtype=torch.int32),
+                  uniforms=torch.rand(B, generator=g))
+        kd = {k: v.cuda() for k, v in kw.items()}
+        out = lm_head_sample(h, w, softcap=cap, return_logprobs=True, return_logits=True, **kd)
+        ref = sample_tokens(out.logits, softcap=cap, return_logprobs=True, **kd)
+        torch.cuda.synchronize()
+        assert out.status.tolist() == [0] * B
+        assert torch.equal(out.tokens, ref.tokens), seed
+        assert torch.equal(out.logprobs.view(torch.int32), ref.logprobs.view(torch.int32)), seed
 
 
 def test_argument_errors():
