@@ -14,7 +14,9 @@ from typing import Optional
 
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflsampler.so")
+# FL_SAMPLER_LIB names another build of the library (the host-sanitizer build).
+LIB_PATH = os.environ.get("FL_SAMPLER_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib",
+                                                            "libflsampler.so")
 
 FL_ABI_VERSION = 5
 FL_DTYPE_F32, FL_DTYPE_BF16, FL_DTYPE_F16 = 0, 1, 2

@@ -37,6 +37,18 @@ HIPCC_FLAGS = [
 ]
 
 
+# The host-sanitizer build: AddressSanitizer and UndefinedBehaviorSanitizer on
+# the host side only (every -fsanitize= behind -Xarch_host; the device code is
+# built as usual, at -O1), linked against the shared sanitizer runtime, which
+# the loading process must preload.  Only the C ABI's host code (argument
+# checks, workspace sizing, launches) runs under it; no kernel is launched
+# without a GPU.
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer", "-g",
+]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -74,6 +86,42 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
+
+
+def asan_runtime() -> str:
+    """The shared AddressSanitizer runtime of ROCm's clang (to preload), or ''."""
+    hits = sorted(glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return hits[-1] if hits else ""
+
+
+def build_sanitized(out_dir: str, verbose: bool = False) -> str:
+    """Build the library with the host sanitizers into ``out_dir``; returns its
+    path.  Load it with FL_SAMPLER_LIB=<path> and the runtime from
+    ``asan_runtime()`` in LD_PRELOAD."""
+    os.makedirs(out_dir, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    flags = [f if f != "-O3" else "-O1" for f in HIPCC_FLAGS]
+    jobs = min(len(srcs), max(1, (os.cpu_count() or 2) // 2), 8)
+
+    def one(src):
+        obj = os.path.join(out_dir, os.path.basename(src) + ".o")
+        cmd = [hipcc(), *flags, *SANITIZE_FLAGS, "-c", src, "-o", obj]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(one, srcs))
+    out = os.path.join(out_dir, "libflsampler.so")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+           "-Xarch_host", "-fsanitize=undefined", "-shared-libsan", *objs, "-o", out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    return out
 
 
 if __name__ == "__main__":
