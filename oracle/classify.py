@@ -21,7 +21,10 @@ oracle's, except for
                             leaves (``_top_p_count_range``);
                  selection  the draw must fall within the doubt of the
                             chosen token's cumulative interval
-                            (``selection_near``); greedy picks must be able to
+                            (``selection_near``); on a soft-capped row, on the
+                            kernel's own filtered values when they are the
+                            oracle's within a few units of the dtype
+                            (``_softcap_selection_near``); greedy picks must be able to
                             win the first-index argmax under ``RK``
                             (``greedy_near``);
                  speculative  accept ratios and residual / bonus draws
@@ -148,9 +151,11 @@ def _top_p_count_range(y: np.ndarray, surv: np.ndarray, grp: np.ndarray, top_p: 
 
 def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tensor, ref_tok: int,
                  got_keep: Optional[torch.Tensor], got_tok: Optional[int], softcap: float = 0.0,
-                 rel: float = REL) -> RowVerdict:
+                 rel: float = REL, got_values: Optional[torch.Tensor] = None) -> RowVerdict:
     """Classify one row.  ``x``: the input row [V]; ``ref_keep``/``got_keep``:
-    bool [V] keep masks (``got_keep`` may be None to check the token only)."""
+    bool [V] keep masks (``got_keep`` may be None to check the token only).
+    ``got_values``: the kernel's filtered values of the row (-inf outside its
+    mask), used only for soft-capped rows (see ``_softcap_selection_near``)."""
     dt = x.dtype
     same_mask = got_keep is None or bool(torch.equal(ref_keep, got_keep))
     if same_mask and (got_tok is None or got_tok == ref_tok):
@@ -234,6 +239,12 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 verdict.kind = "NEAR"
                 margins.append(m)
                 verdict.details.append(f"near selection: token {got_tok} vs {ref_tok}, margin {m:.3g}")
+            elif softcap > 0 and p.temperature > 0 and got_values is not None and \
+                    _softcap_selection_near(y, got_values, keep, u, got_tok, dt):
+                verdict.kind = "NEAR"
+                margins.append(m)
+                verdict.details.append(f"near selection on the kernel's soft-capped values: token {got_tok} vs "
+                                       f"{ref_tok}, distance {m:.3g} on the oracle's")
             else:
                 verdict.kind = "MISMATCH"
                 verdict.details.append(f"token {got_tok} vs oracle {ref_tok} (expected {expect} on got mask), "
@@ -285,6 +296,31 @@ def selection_near(filt: torch.Tensor, u: float, got_tok: int) -> tuple:
     lo, hi = (c[j - 1], d[j - 1]) if j > 0 else (0.0, 0.0), (c[j], d[j])
     dist = max(0.0, lo[0] - t, t - hi[0])
     return bool(lo[0] - lo[1] <= t < hi[0] + hi[1]), dist
+
+
+SOFTCAP_ULPS = {torch.float32: 8, torch.bfloat16: 2, torch.float16: 2}
+
+
+def _softcap_selection_near(y: np.ndarray, got_values: torch.Tensor, keep: np.ndarray, u: float, got_tok: int,
+                            dt) -> bool:
+    """A soft-capped row whose draw lies among values the soft-cap saturates
+    (or nearly so): there the kernels' tanh and the CPU's may round a value
+    to neighbouring representable numbers, which reorders near-equal values
+    and moves the draw by whole elements.  Accepted when the kernel's
+    filtered values are the oracle's ``y`` within ``SOFTCAP_ULPS`` units of
+    the dtype on the kept elements (exactly -inf elsewhere) and the draw lies
+    within the rounding doubt of ``got_tok``'s interval on the kernel's own
+    values."""
+    g = got_values.to(dt).double().numpy()
+    if not np.array_equal(np.isfinite(g), keep):
+        return False
+    mant = {torch.float32: 23, torch.bfloat16: 7, torch.float16: 10}[dt]
+    yk, gk = y[keep], g[keep]
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(yk), 2.0 ** -126))) - mant)
+    if yk.size == 0 or float(np.max(np.abs(gk - yk) / ulp)) > SOFTCAP_ULPS[dt]:
+        return False
+    ok, _ = selection_near(torch.from_numpy(g).to(dt), u, got_tok)
+    return ok
 
 
 def greedy_near(filt: torch.Tensor, got_tok: int, expect: int) -> tuple:

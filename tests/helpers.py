@@ -33,7 +33,8 @@ def oracle_rows(w) -> List[O.RowResult]:
 
 
 def classify_workload(w, got_tokens: torch.Tensor, got_keep: torch.Tensor = None,
-                      ref: List[O.RowResult] = None) -> Tuple[dict, List[C.RowVerdict]]:
+                      ref: List[O.RowResult] = None,
+                      got_values: torch.Tensor = None) -> Tuple[dict, List[C.RowVerdict]]:
     ref = ref if ref is not None else oracle_rows(w)
     x = w.logits.cpu()
     toks = got_tokens.cpu().tolist()
@@ -41,8 +42,9 @@ def classify_workload(w, got_tokens: torch.Tensor, got_keep: torch.Tensor = None
     for b in range(w.batch):
         rk = ~torch.isneginf(ref[b].filtered.float())
         gk = None if got_keep is None else got_keep[b]
+        gv = None if got_values is None else got_values[b].cpu()
         verdicts.append(C.classify_row(x[b], row_params(w, b), float(w.uniforms[b]), rk, ref[b].token, gk, toks[b],
-                                       softcap=w.softcap))
+                                       softcap=w.softcap, got_values=gv))
     return C.summarise(verdicts), verdicts
 
 

@@ -315,3 +315,44 @@ def test_spec_bonus_at_an_open_top_p_cut():
     assert kind(order[lo - 1]) == "MISMATCH"
     assert kind(order[hi + 1]) == "MISMATCH"
     assert kind(order[(hi + 100) % len(order)]) == "MISMATCH"
+
+
+def test_softcap_saturated_draw_on_the_kernels_values():
+    """A float32 row far beyond its soft-cap (x ~ N(0, 60^2), cap 5, T 0.1):
+    thousands of values sit at the cap, where a kernel's tanh may round a
+    value one unit below the CPU's.  Such a unit reorders the near-equal
+    values and moves the draw by whole elements.  With the kernel's filtered
+    values (here: the oracle's, a third of the values at the cap moved one
+    unit down) a draw made on them is NEAR; without them it is not accepted;
+    the next element of their order, or values 20 units away, are MISMATCH."""
+    V, cap = 50257, 5.0
+    g = torch.Generator().manual_seed(3)
+    x = 60.0 * torch.randn(V, generator=g)
+    p = O.RowParams(temperature=0.1)
+    top = None
+    for k in range(64):
+        u = float(torch.rand(1, generator=g))
+        r, keep, y = _oracle(x, p, u, softcap=cap)
+        at_cap = torch.nonzero(y == y.max()).flatten()
+        moved = y.clone()
+        sub = at_cap[torch.randperm(at_cap.numel(), generator=g)[: at_cap.numel() // 3]]
+        moved[sub] = torch.nextafter(moved[sub], torch.tensor(float("-inf")))
+        tok = O.select_token(moved, u, p.temperature)
+        if tok != r.token:
+            top = (u, r, keep, y, moved, tok)
+            break
+    assert top is not None, "no draw moved by the perturbation"
+    u, r, keep, y, moved, tok = top
+    assert _kind(x, p, u, keep, r.token, keep, tok, softcap=cap).kind == "MISMATCH"
+    v = C.classify_row(x, p, u, keep, r.token, keep, tok, softcap=cap, got_values=moved)
+    assert v.kind == "NEAR", v.details
+    order = O.selection_order(moved).tolist()
+    nxt = order[order.index(tok) + 1]
+    v = C.classify_row(x, p, u, keep, r.token, keep, nxt, softcap=cap, got_values=moved)
+    assert v.kind == "MISMATCH", v.details
+    far = moved.clone()
+    far[sub] = far[sub] - 20 * 2.0 ** -23 * far[sub].abs()
+    tok_far = O.select_token(far, u, p.temperature)
+    assert tok_far != r.token
+    v = C.classify_row(x, p, u, keep, r.token, keep, tok_far, softcap=cap, got_values=far)
+    assert v.kind == "MISMATCH", v.details

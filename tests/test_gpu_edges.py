@@ -3,14 +3,15 @@ vocabularies of 1, 2, 3, 8 and 65 values in every dtype, with top-k above
 and at the vocabulary, min-p, top-p, penalties below and above 1 and greedy
 rows; logits given as a strided view (rows of a wider buffer), which must
 sample like their contiguous copy; a soft-cap whose x / cap spans both
-branches of the kernels' tanh; and float32 rows saturated by the soft-cap."""
+branches of the kernels' tanh; and float32 rows saturated by the soft-cap,
+whose draws fall among thousands of values at the cap."""
 
 import pytest
 import torch
 
 from rl_project_amd import filtered_outputs, sample_tokens, workloads
 from oracle import sampler_oracle as O
-from tests.helpers import classify_workload
+from tests.helpers import classify_workload, unpack_mask
 
 pytestmark = pytest.mark.gpu
 
@@ -124,5 +125,34 @@ def test_float32_rows_saturated_by_the_softcap():
     torch.cuda.synchronize()
     assert out.status.tolist() == [0] * B
     summ, verdicts = classify_workload(w, out.tokens.cpu())
+    print(f"   {summ}", flush=True)
+    assert summ["MISMATCH"] == 0, [(b, v.details) for b, v in enumerate(verdicts) if not v.ok][:4]
+
+
+def test_float32_draws_among_values_at_the_softcap():
+    """x ~ N(0, 60^2), cap 5, T 0.1: nearly a quarter of each row sits at the cap
+    (tanh rounds to 1), and the draws fall among those values.  The kernels'
+    tanh may round a value there one unit below the CPU's, which reorders
+    near-equal values and moves a draw by whole elements; the classifier then
+    checks the draw on the kernels' own filtered values, after checking that
+    they are the oracle's within a few units.  Every row classifies."""
+    B, V, cap = 64, 50257, 5.0
+    print(f"[edges draws at the softcap] B={B} V={V} cap={cap}", flush=True)
+    g = torch.Generator().manual_seed(29)
+    x = 60.0 * torch.randn(B, V, generator=g)
+    T = torch.full((B,), 0.1)
+    K = torch.zeros(B, dtype=torch.int32)
+    P = torch.tensor([0.9, 1.0, 0.5, 0.99] * (B // 4))
+    MP, RP = torch.zeros(B), torch.ones(B)
+    U = torch.rand(B, generator=g)
+    w = workloads.SampleWorkload("edges_softcap_draws", x, T, K, P, MP, RP, None, None, U, softcap=cap)
+    wd = w.to("cuda")
+    out = sample_tokens(wd.logits, **wd.kwargs())
+    kw = wd.kwargs()
+    kw.pop("uniforms")
+    filt, _, mask, status = filtered_outputs(wd.logits, want_filtered=True, want_mask=True, **kw)
+    torch.cuda.synchronize()
+    assert out.status.tolist() == [0] * B and status.tolist() == [0] * B
+    summ, verdicts = classify_workload(w, out.tokens.cpu(), unpack_mask(mask, V), got_values=filt.cpu())
     print(f"   {summ}", flush=True)
     assert summ["MISMATCH"] == 0, [(b, v.details) for b, v in enumerate(verdicts) if not v.ok][:4]

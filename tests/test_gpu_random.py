@@ -70,7 +70,7 @@ def test_random_sampling_cases(first):
         torch.cuda.synchronize()
         assert int(status.abs().sum()) == 0, (seed, status.tolist())
         refs = oracle_rows(w)
-        summ, verdicts = classify_workload(w, out.tokens, unpack_mask(mask, w.vocab), ref=refs)
+        summ, verdicts = classify_workload(w, out.tokens, unpack_mask(mask, w.vocab), ref=refs, got_values=filt.cpu())
         for b, v in enumerate(verdicts):
             assert v.ok, (seed, b, v.details[:3])
             counts[v.kind] = counts.get(v.kind, 0) + 1
