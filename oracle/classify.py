@@ -316,7 +316,7 @@ def _softcap_selection_near(y: np.ndarray, got_values: torch.Tensor, keep: np.nd
         return False
     mant = {torch.float32: 23, torch.bfloat16: 7, torch.float16: 10}[dt]
     yk, gk = y[keep], g[keep]
-    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(yk), 2.0 ** -126))) - mant)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(yk), torch.finfo(dt).tiny))) - mant)
     if yk.size == 0 or float(np.max(np.abs(gk - yk) / ulp)) > SOFTCAP_ULPS[dt]:
         return False
     ok, _ = selection_near(torch.from_numpy(g).to(dt), u, got_tok)
