@@ -16,6 +16,13 @@ K back-to-back launches, against the algorithmic bytes of one launch and
 MI355X's 8 TB/s HBM peak), and the CPU
 baseline (the oracle's per-row restatement of the reference sampler, timed on
 this host on a bounded sample of the same workload).
+
+The default run then times the other configurations (B=64 V=32000 fp32 with
+stop ids; B=512 V=262144 soft-capped fp32; speculative verify of 32 x 5
+drafts at V=128256) with shorter timed regions, each under ``configs`` in
+the same line with its own roofline, CPU baseline and parity counts
+(``--headline-only`` skips them).  ``roofline.traffic`` is read from the
+committed counter profile of the workload (``traffic_source`` says which).
 """
 
 from __future__ import annotations
@@ -32,18 +39,35 @@ ISOLATED = 20  # launches timed one by one for the spread
 METRIC = "sampled rows/sec at B=256,V=128256 mixed params; achieved HBM GB/s vs peak"
 DEFAULT_WORKLOAD = "hetero_bf16_256x128256"
 MALL_BYTES = 256 * 1024 * 1024
+# timed after the headline in the default run, each with its own roofline
+OTHER_CONFIGS = ("uniform_f32_64x32000", "softcap_zipf_f32_512x262144", "spec_f32_32x5x128256")
 
 
 def _traffic_from_profile(workload: str):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    scaled by the copy-kernel calibration), as recorded under profiles/."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{workload}_traffic.txt")
+    scaled by the copy-kernel calibration), as recorded under profiles/ -- not
+    measured in this run (counters need a profiler run of their own).
+    Returns (bytes or None, source description)."""
+    rel = os.path.join("profiles", f"{workload}_traffic.txt")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
     if not os.path.exists(path):
-        return None
+        return None, "no counter profile recorded for this workload"
+    val, date = None, ""
     for line in open(path):
         if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+            val = float(line.split(":", 1)[1])
+        elif line.startswith("measured:"):
+            date = line.split(":", 1)[1].strip()
+    return val, f"{rel} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of an earlier build, not this run" + \
+        (f"; {date}" if date else "") + ")"
+
+
+def _roofline(alg_bytes: int, ms: float, workload: str, **extra) -> dict:
+    achieved = alg_bytes / (ms * 1e-3) / 1e9
+    traffic, src = _traffic_from_profile(workload)
+    return dict({"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": src,
+                 "algorithmic_bytes": alg_bytes}, **extra)
 
 
 def _timed_region(torch, dev, stream, K: int, launch):
@@ -205,10 +229,11 @@ def cpu_baseline_spec(w, seconds: float, got=None):
                       f"{dt:.1f} s"}
 
 
-def bench_spec(args, dev) -> int:
+def bench_spec(args, dev, name: str, steps: int, warmup: int, cpu_seconds: float):
     """Speculative verify: one step = the three launches of one batch (target
     rows with the bonus draw, draft rows, verify); tokens/s counts accepted
-    drafts plus the resampled or bonus token of every sequence."""
+    drafts plus the resampled or bonus token of every sequence.  Returns the
+    result dict, or None when a row failed."""
     import torch
 
     from rl_project_amd import sample_tokens, workloads
@@ -218,41 +243,40 @@ def bench_spec(args, dev) -> int:
         # drafts drawn from the filtered draft distribution by the GPU sampler
         return sample_tokens(rows.to(dev), temperature=0.8, top_p=0.95, uniforms=u.to(dev)).tokens.cpu()
 
-    ws = [workloads.make_spec(args.workload, seed=0, draft_sampler=draft_sampler)]
+    ws = [workloads.make_spec(name, seed=0, draft_sampler=draft_sampler)]
     batch_bytes = (ws[0].target.numel() + ws[0].draft.numel()) * ws[0].target.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))
     for s in range(1, nbuf):
-        ws.append(workloads.make_spec(args.workload, seed=s, draft_sampler=draft_sampler))
+        ws.append(workloads.make_spec(name, seed=s, draft_sampler=draft_sampler))
     plans = []
     for w in ws:
         wd = w.to(dev)
         plans.append(SpecPlan(wd.target, wd.draft, wd.draft_ids, temperature=wd.temperature, top_p=wd.top_p,
                               u_accept=wd.u_accept, u_resample=wd.u_resample, return_ratio=False))
     stream = torch.cuda.current_stream(dev)
-    for i in range(max(args.warmup, nbuf)):
+    for i in range(max(warmup, nbuf)):
         plans[i % nbuf].launch()
     torch.cuda.synchronize(dev)
     for pl in plans:
         if not bool(pl.status_ok().all()):
-            print("speculative rows failed", file=sys.stderr)
-            return 1
+            print(f"{name}: speculative rows failed", file=sys.stderr)
+            return None
     toks = [int((pl.n_accepted + 1).sum()) for pl in plans]
 
-    K = args.steps
+    K = steps
     step_ms, wall = _timed_region(torch, dev, stream, K, lambda k: plans[k % nbuf].launch())
     durs = _isolated_launches(torch, dev, stream, lambda k: plans[k % nbuf].launch())
     w = ws[0]
     B, Kd = w.draft_ids.shape
     n_tok = sum(toks[k % nbuf] for k in range(K))
     alg_bytes = w.algorithmic_bytes()
-    achieved = alg_bytes / (step_ms * 1e-3) / 1e9
     result = {
         "metric": f"speculative verify tokens/sec at B={B}, K={Kd}, V={w.target.size(2)} fp32 (accepted + 1 per sequence)",
         "value": n_tok / wall,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": K,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": wall * 1e3 / K,
         "higher_is_better": True,
         "scaling": "weak",
@@ -261,21 +285,18 @@ def bench_spec(args, dev) -> int:
         "data": "synthetic",
         "config": {"workload": w.name, "sequences": B, "drafts": Kd, "vocab": w.target.size(2),
                    "input_buffers": nbuf, "tokens_per_step_mean": n_tok / K, "sequences_per_s": B * K / wall},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
-                     "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
-                     "isolated_step_ms_p10": durs[len(durs) // 10],
-                     "isolated_step_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": "k_sample_rows32 (target rows) + k_sample_rows32 (draft rows) + k_spec_verify"},
+        "roofline": _roofline(alg_bytes, step_ms, w.name, step_ms_mean=step_ms,
+                              isolated_step_ms_p10=durs[len(durs) // 10],
+                              isolated_step_ms_p90=durs[(9 * len(durs)) // 10],
+                              kernel="k_sample_rows32 (target and draft rows) + k_spec_verify"),
     }
     if not args.no_cpu_baseline:
         torch.cuda.synchronize(dev)
         plans[0].launch()      # the first batch's own outputs, checked against the oracle
         torch.cuda.synchronize(dev)
-        result["cpu_baseline"] = cpu_baseline_spec(w, args.cpu_seconds, (plans[0].n_accepted, plans[0].tokens))
+        result["cpu_baseline"] = cpu_baseline_spec(w, cpu_seconds, (plans[0].n_accepted, plans[0].tokens))
         result["parity"] = result["cpu_baseline"]["parity"]
-    print(json.dumps(result), flush=True)
-    return 0
+    return result
 
 
 def bench_rowstats(args, dev) -> int:
@@ -312,19 +333,17 @@ def bench_rowstats(args, dev) -> int:
     kern_ms, wall = _timed_region(torch, dev, stream, K, launch)
     durs = _isolated_launches(torch, dev, stream, launch)
     alg_bytes = per_buf + R * (8 + 4 + 4 + (4 if kl else 0))
-    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     result = {
         "metric": f"token log-prob + entropy{' + KL' if kl else ''} rows/sec over {R}x{V} {parts[1]} logits",
         "value": R * K / wall, "unit": "rows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
         "ms_per_step": wall * 1e3 / K, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": parts[1], "data": "synthetic",
         "config": {"workload": args.workload, "rows": R, "vocab": V, "kl": kl, "input_buffers": nbuf},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(args.workload),
-                     "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
-                     "isolated_launch_ms_p10": durs[len(durs) // 10],
-                     "isolated_launch_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": f"k_row_stats<{ {'bf16': 'BF16', 'f16': 'F16', 'f32': 'F32'}[parts[1]] }, {str(kl).lower()}>"},
+        "roofline": _roofline(alg_bytes, kern_ms, args.workload, kernel_ms_mean=kern_ms,
+                              isolated_launch_ms_p10=durs[len(durs) // 10],
+                              isolated_launch_ms_p90=durs[(9 * len(durs)) // 10],
+                              kernel=f"k_row_stats<{ {'bf16': 'BF16', 'f16': 'F16', 'f32': 'F32'}[parts[1]] }, "
+                                     f"{str(kl).lower()}>"),
     }
     if not args.no_cpu_baseline:
         # the oracle (the reference's torch expressions) on the host, on the first rows
@@ -389,7 +408,7 @@ def bench_lmhead(args, dev) -> int:
     durs = _isolated_launches(torch, dev, stream, lambda k: plan.launch())
     # the unfused step: GEMM into logits, then fl_sample
     logits = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
-    splan = SamplerPlan(logits, **kd)
+    splan = SamplerPlan(logits, exact_repeat=False, **kd)   # (rows checked: status 0)
 
     def unfused(k):
         torch.matmul(h, W.t(), out=logits)
@@ -399,7 +418,6 @@ def bench_lmhead(args, dev) -> int:
     unf_ms, _ = _timed_region(torch, dev, stream, K, unfused)
     gemm_ms, _ = _timed_region(torch, dev, stream, K, lambda k: torch.matmul(h, W.t(), out=logits))
     alg_bytes = V * D * 2 + B * D * 2 + B * 16
-    achieved = alg_bytes / (step_ms * 1e-3) / 1e9
     flops = 2.0 * B * D * V
     result = {
         "metric": f"decode steps/sec: lm_head + sampling of {B} rows, D={D}, V={V} (bf16), no [B,V] logits in HBM",
@@ -408,13 +426,11 @@ def bench_lmhead(args, dev) -> int:
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": args.workload, "batch": B, "dim": D, "vocab": V, "history": 2048,
                    "tokens_per_s": B * K / wall},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(args.workload),
-                     "algorithmic_bytes": alg_bytes, "step_ms_mean": step_ms,
-                     "isolated_step_ms_p10": durs[len(durs) // 10],
-                     "isolated_step_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": "k_lm_prep + k_lm_sample + k_lm_thresh + k_lm_gemm + k_lm_pick",
-                     "mfma_tflops": flops / (step_ms * 1e-3) / 1e12, "mfma_peak_tflops": 2500.0},
+        "roofline": _roofline(alg_bytes, step_ms, args.workload, step_ms_mean=step_ms,
+                              isolated_step_ms_p10=durs[len(durs) // 10],
+                              isolated_step_ms_p90=durs[(9 * len(durs)) // 10],
+                              kernel="k_lm_prep + k_lm_sample + k_lm_thresh + k_lm_gemm + k_lm_pick",
+                              mfma_tflops=flops / (step_ms * 1e-3) / 1e12, mfma_peak_tflops=2500.0),
         "unfused": {"ms_per_step": unf_ms, "matmul_ms": gemm_ms,
                     "note": "torch.matmul(h, W.T) into [B, V] bf16 logits, then fl_sample (SamplerPlan)"},
     }
@@ -461,6 +477,11 @@ def main() -> int:
     ap.add_argument("--buffers", type=int, default=0, help="distinct input batches (default: > 256 MB in total)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time (3 segments; a fourth on 1 thread)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the default workload (skip the other configurations)")
+    ap.add_argument("--other-steps", type=int, default=50, help="timed steps of each other configuration")
+    ap.add_argument("--other-cpu-seconds", type=float, default=6.0,
+                    help="CPU baseline time of each other configuration")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run an elementwise read+write kernel (torch.neg) over MIB MiB, 5 launches: the "
                          "known-size kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -473,9 +494,6 @@ def main() -> int:
         return 2
 
     import torch
-
-    from rl_project_amd import workloads
-    from rl_project_amd.sampling import SamplerPlan
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -491,60 +509,105 @@ def main() -> int:
         print(json.dumps({"calibrate_copy_bytes": 4 * n, "launches": 5}), flush=True)
         return 0
     if args.workload.startswith("spec_"):
-        return bench_spec(args, dev)
+        res = bench_spec(args, dev, args.workload, args.steps, args.warmup, args.cpu_seconds)
+        if res is None:
+            return 1
+        print(json.dumps(res), flush=True)
+        return 0
     if args.workload.startswith("rowstats_"):
         return bench_rowstats(args, dev)
     if args.workload.startswith("lmhead_"):
         return bench_lmhead(args, dev)
-    w = workloads.make(args.workload, seed=0)
+    result = bench_rows(args, dev, args.workload, args.steps, args.warmup, args.cpu_seconds)
+    if result is None:
+        return 1
+    result["metric"] = METRIC if args.workload == DEFAULT_WORKLOAD else result["metric"]
+    if args.workload == DEFAULT_WORKLOAD and not args.headline_only:
+        # the other configurations, after the headline's timed region, with
+        # shorter timed regions and CPU samples: each its own roofline and
+        # parity counts
+        import torch
+
+        result["configs"] = {}
+        for name in OTHER_CONFIGS:
+            torch.cuda.empty_cache()
+            t0 = time.perf_counter()
+            if name.startswith("spec_"):
+                r = bench_spec(args, dev, name, args.other_steps, 5, args.other_cpu_seconds)
+            else:
+                r = bench_rows(args, dev, name, args.other_steps, 5, args.other_cpu_seconds)
+            if r is None:
+                return 1
+            r["bench_seconds"] = time.perf_counter() - t0
+            for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "data"):
+                r.pop(k, None)
+            result["configs"][name] = r
+            print(f"{name}: {r['value']:.4g} {r['unit']}, {r['ms_per_step']:.4f} ms/step", file=sys.stderr,
+                  flush=True)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_rows(args, dev, name: str, steps: int, warmup: int, cpu_seconds: float):
+    """One step = one fl_sample launch over a batch of workload ``name``
+    (input batches rotated past the Infinity Cache).  Returns the result dict,
+    or None when a row of any rotated batch reports a status bit."""
+    import torch
+
+    from rl_project_amd import workloads
+    from rl_project_amd.sampling import SamplerPlan
+
+    w = workloads.make(name, seed=0)
     batch_bytes = w.logits.numel() * w.logits.element_size()
     nbuf = args.buffers or max(2, math.ceil(1.25 * MALL_BYTES / batch_bytes))
     wd = w.to(dev)
     bufs = [wd.logits]
     for s in range(1, nbuf):
-        bufs.append(workloads.make(args.workload, seed=s).logits.to(dev))
+        bufs.append(workloads.make(name, seed=s).logits.to(dev))
     kw = wd.kwargs()
-    plans = [SamplerPlan(buf, **kw) for buf in bufs]
+    # (no exact-count repeat: every row of every rotated batch is checked
+    # below for FL_ROW_LIMIT, the only status the repeat would act on)
+    plans = [SamplerPlan(buf, exact_repeat=False, **kw) for buf in bufs]
     stream = torch.cuda.current_stream(dev)
 
-    for i in range(args.warmup):
+    for i in range(max(warmup, nbuf)):
         plans[i % nbuf].launch()
     torch.cuda.synchronize(dev)
-    status = plans[0].output.status
-    if int((status != 0).sum()):
-        print(f"rows failed: status {status.tolist()[:16]}", file=sys.stderr)
-        return 1
+    for j, pl in enumerate(plans):
+        status = pl.output.status
+        if int((status != 0).sum()):
+            print(f"{name}: rows of batch {j} failed: status {status.tolist()[:16]}", file=sys.stderr)
+            return None
 
-    K = args.steps
+    K = steps
     kern_ms, wall = _timed_region(torch, dev, stream, K, lambda k: plans[k % nbuf].launch())
     durs = _isolated_launches(torch, dev, stream, lambda k: plans[k % nbuf].launch())
 
     B = w.batch
     alg_bytes = w.algorithmic_bytes()
-    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
-    ms_per_step = wall * 1e3 / K
+    dtype = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w.logits.dtype]
     result = {
-        "metric": METRIC,
+        "metric": f"sampled rows/sec at B={B},V={w.vocab} ({name}); achieved HBM GB/s vs peak",
         "value": B * K / wall,
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": K,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "warmup": warmup,
+        "ms_per_step": wall * 1e3 / K,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w.logits.dtype],
+        "dtype": dtype,
         "data": "synthetic",
         "config": {"workload": w.name, "batch": B, "vocab": w.vocab,
                    "history": 0 if w.history is None else int(w.history.size(1)),
-                   "input_buffers": nbuf, "tokens_per_s": B * K / wall},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profile(w.name),
-                     "algorithmic_bytes": alg_bytes, "kernel_ms_mean": kern_ms,
-                     "isolated_launch_ms_p10": durs[len(durs) // 10],
-                     "isolated_launch_ms_p90": durs[(9 * len(durs)) // 10],
-                     "kernel": "k_sample_rows16<BF16, false>" if w.logits.element_size() == 2 else "k_sample_rows32"},
+                   "input_buffers": nbuf, "tokens_per_s": B * K / wall,
+                   "status_checked": f"every row of all {nbuf} rotated batches: 0"},
+        "roofline": _roofline(alg_bytes, kern_ms, w.name, kernel_ms_mean=kern_ms,
+                              isolated_launch_ms_p10=durs[len(durs) // 10],
+                              isolated_launch_ms_p90=durs[(9 * len(durs)) // 10],
+                              kernel=f"k_sample_rows16<{dtype.upper()}, {str(w.softcap > 0).lower()}>"
+                              if w.logits.element_size() == 2 else "k_sample_rows32"),
     }
     if not args.no_cpu_baseline:
         from rl_project_amd import filtered_outputs
@@ -553,10 +616,10 @@ def main() -> int:
         kw_mask.pop("uniforms")
         _, _, mask0, _ = filtered_outputs(bufs[0], want_filtered=False, want_mask=True, **kw_mask)
         torch.cuda.synchronize(dev)
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, plans[0].output.tokens.clone(), mask0)
+        result["cpu_baseline"] = cpu_baseline(w, cpu_seconds, plans[0].output.tokens.clone(), mask0)
         result["parity"] = result["cpu_baseline"]["parity"]
-    print(json.dumps(result), flush=True)
-    return 0
+    del plans, bufs, wd
+    return result
 
 
 if __name__ == "__main__":

@@ -149,6 +149,52 @@ def _top_p_count_range(y: np.ndarray, surv: np.ndarray, grp: np.ndarray, top_p: 
     return lo_n, hi_n, float(c_ref[j0] - ps[j0]) if pos.size else 0.0
 
 
+def _min_p_survivor_sets(pre_minp: np.ndarray, probs: np.ndarray, min_p: float, dt, cap: int = 8) -> List[np.ndarray]:
+    """The min-p survivor sets (bool [V]) that the rounding doubt leaves open
+    (``sampling.py:40-43``): the oracle's first, then the others.
+
+    min-p keeps ``round(e r) >= round(round(r) min_p)`` with ``r = 1/sum(e)``
+    over the top-k survivors ``pre_minp`` (float64, -inf where removed); the
+    test is monotone in ``e``, so the survivors are a prefix of the distinct
+    values in descending order.  A value's decision is open when it flips
+    under the kernels' relative rounding ``RK`` of ``e`` or ``r``, or when the
+    oracle's own softmax output (``probs``) decides it otherwise.  Every prefix
+    whose boundary lies in the band of open values is a survivor set a
+    correct kernel may reach; a top-p cut is then judged on the set the kernel
+    used, since its cumulative sums run over those survivors."""
+    fin = np.isfinite(pre_minp)
+    vals = np.unique(pre_minp[fin])[::-1]
+    M = float(vals[0])
+    e = np.exp(vals - M)
+    S = float(np.exp(pre_minp[fin] - M).sum())
+    r = 1.0 / S
+    mp = np.float32(min_p)
+
+    def keep(e_, r_):
+        return _rn(e_ * r_, dt) >= _rn(_rn(np.array([r_]), dt) * mp, dt)[0]
+
+    exact = keep(e, r)
+    flips = np.zeros(vals.size, dtype=bool)
+    for fe, fr in ((1 - 4 * RK, 1.0), (1 + 4 * RK, 1.0), (1.0, 1 - 4 * RK), (1.0, 1 + 4 * RK)):
+        flips |= keep(e * fe, r * fr) != exact
+    # the oracle's decision per distinct value: its softmax output at a member
+    first = {}
+    idx = np.nonzero(fin)[0]
+    for i in idx[np.unique(pre_minp[idx], return_index=True)[1]]:
+        first[pre_minp[i]] = i
+    thr_or = _rn(np.array([probs.max() * mp]), dt)[0]
+    oracle = np.array([probs[first[v]] >= thr_or for v in vals])
+    open_ = flips | (oracle != exact)
+    n_sure = int(np.argmax(~(exact & ~open_))) if not (exact & ~open_).all() else vals.size
+    n_max = int(np.nonzero(exact | open_)[0].max()) + 1 if (exact | open_).any() else 0
+    n_or = int(oracle.sum())
+    sets = [fin & (pre_minp >= vals[n_or - 1])] if n_or > 0 else [np.zeros_like(fin)]
+    for n in range(max(n_sure, 1), min(n_max, n_sure + cap) + 1):
+        if n != n_or:
+            sets.append(fin & (pre_minp >= vals[n - 1]))
+    return sets
+
+
 def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tensor, ref_tok: int,
                  got_keep: Optional[torch.Tensor], got_tok: Optional[int], softcap: float = 0.0,
                  rel: float = REL, got_values: Optional[torch.Tensor] = None) -> RowVerdict:
@@ -176,6 +222,7 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
         pre_minp = stage.clone()
         stage = O._min_p(stage, p.min_p or None)
         surv = ~np.isneginf(stage[0].double().numpy())
+        minp_sets = None
         for v in np.unique(y[diff]):
             grp = np.nonzero(y == v)[0]
             nr, ng = int(ref_keep[grp].sum()), int(got_keep[grp].sum())
@@ -210,13 +257,25 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                 del probs
             # top-p boundary: the group's kept count must lie in the range
             # that the rounding doubt of the cumulative sums leaves open
+            # (on every min-p survivor set the rounding doubt allows: the
+            # kernel's cumulative sums run over the survivors it kept)
             if not explained and p.top_p is not None and 0 < p.top_p < 1:
-                lo_n, hi_n, excl = _top_p_count_range(y, surv, grp, p.top_p, dt)
-                if lo_n <= ng <= hi_n:
-                    explained = True
-                    margins.append(abs(excl - p.top_p) / max(p.top_p, 1e-30))
-                    verdict.details.append(f"near top-p y={v:.9g} excl={excl:.9g} top_p={p.top_p} "
-                                           f"kept {ng} in [{lo_n}, {hi_n}]")
+                sets = [surv]
+                if p.min_p and p.min_p > 0:
+                    if minp_sets is None:
+                        pm = pre_minp[0].double().numpy()
+                        minp_sets = _min_p_survivor_sets(pm, F.softmax(pre_minp, dim=-1)[0].double().numpy(),
+                                                         p.min_p, dt)[1:]
+                    sets = sets + minp_sets
+                for k, s in enumerate(sets):
+                    lo_n, hi_n, excl = _top_p_count_range(y, s, grp, p.top_p, dt)
+                    if lo_n <= ng <= hi_n:
+                        explained = True
+                        margins.append(abs(excl - p.top_p) / max(p.top_p, 1e-30))
+                        verdict.details.append(f"near top-p y={v:.9g} excl={excl:.9g} top_p={p.top_p} "
+                                               f"kept {ng} in [{lo_n}, {hi_n}]" +
+                                               (f" (min-p survivors: open set {k})" if k else ""))
+                        break
             if not explained:
                 verdict.kind = "MISMATCH"
                 verdict.details.append(f"mask group y={v:.9g} n={grp.size}: ref kept {nr}, got kept {ng}")

@@ -125,11 +125,15 @@ __device__ __forceinline__ float f32_of_key(uint32_t k) {
 // [0, 0.625) it lies within 0.75 ulp of tanh, equals the correctly rounded
 // value for all but 0.04 % of them, and is monotone (an exhaustive check
 // against double-precision tanh runs in the CPU tests).  The odd form makes
-// it exactly antisymmetric.  Larger |z| take tanhf.  A logit row's values,
-// divided by a soft-cap such as 30, fall in the polynomial's range, where a
-// wave then runs this branch alone.
+// it exactly antisymmetric.  Larger |z| take tanhf, floored in magnitude at
+// the polynomial's value at the largest float below 0.625 (which is the
+// correctly rounded tanh(0.625); the CPU test checks the constant), so that
+// a tanhf an ulp low at the switch cannot make the function decrease there.
+// A logit row's values, divided by a soft-cap such as 30, fall in the
+// polynomial's range, where a wave then runs this branch alone.
 constexpr float TANH_P[6] = {-0.33333330807135236f, 0.13333206186821212f, -0.05394678612676864f,
                              0.021700831796483553f, -0.008177720758405421f, 0.00214326075575256f};
+constexpr uint32_t TANH_AT_SWITCH_BITS = 0x3f0dfa3fu;  // poly(nextafter(0.625, 0)) = 0.5545997
 __device__ __forceinline__ float fl_tanh(float z) {
   if (fabsf(z) < 0.625f) {
     const float t = z * z;
@@ -140,7 +144,10 @@ __device__ __forceinline__ float fl_tanh(float z) {
     p = __builtin_fmaf(t, p, TANH_P[0]);
     return __builtin_fmaf(z * t, p, z);
   }
-  return tanhf(z);
+  // (a compare and select, not fmaxf: a NaN stays NaN)
+  const float a = fabsf(tanhf(z));
+  const float lo = __uint_as_float(TANH_AT_SWITCH_BITS);
+  return copysignf(a < lo ? lo : a, z);
 }
 
 // soft-cap tanh(x / c) * c  (models/attention/causal.py:109-110): three ops.

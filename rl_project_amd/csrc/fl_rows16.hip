@@ -1291,11 +1291,12 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       if (tok < 0) status |= FL_ROW_LIMIT;
     }
     if (status != 0) tok = -1;
+    // (read before any output is written: out_finished may be finished_in)
+    const bool was_finished = a.finished_in != nullptr && a.finished_in[b] != 0;
     if (a.out_token) a.out_token[b] = tok;
     if (a.out_status) a.out_status[b] = status;
     if (a.out_finished) {
-      const bool fin = (a.finished_in != nullptr && a.finished_in[b] != 0) ||
-                       (tok >= 0 && is_stop(a.stop_ids, a.stop_ld, a.n_stop, b, tok));
+      const bool fin = was_finished || (tok >= 0 && is_stop(a.stop_ids, a.stop_ld, a.n_stop, b, tok));
       a.out_finished[b] = fin ? 1 : 0;
     }
     if (a.out_logprob) {
@@ -1306,8 +1307,8 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       if (tok >= 0) lp = D::rn((y_sel - M) - D::rn(logf(D::rn(static_cast<float>(SK)))));
       a.out_logprob[b] = lp;
     }
-    if ((a.flags & FL_FLAG_APPEND_HISTORY) && hist_rows && tok >= 0 &&
-        !(a.finished_in != nullptr && a.finished_in[b] != 0) && H_in >= 0 && H_in < a.hist_ld) {
+    if ((a.flags & FL_FLAG_APPEND_HISTORY) && hist_rows && tok >= 0 && !was_finished && H_in >= 0 &&
+        H_in < a.hist_ld) {
       // (every read of this row's history, all below index H_in, finished
       // before the barriers that led here)
       const_cast<int32_t*>(a.hist_ids)[b * a.hist_ld + H_in] = static_cast<int32_t>(tok);

@@ -57,7 +57,10 @@ class LmHeadPlan:
             raise NotImplementedError("the fused lm_head path takes bf16 hidden states and weights")
         if not hidden.is_cuda or hidden.device != weight.device:
             raise ValueError("hidden and weight must be on the same GPU")
-        if hidden.stride(1) != 1:
+        # (the kernels address the hidden states with 32-bit offsets: a
+        # strided view whose rows span more than 2^29 elements, such as the
+        # last position of [B, T, D] prefill states, is copied first)
+        if hidden.stride(1) != 1 or (hidden.size(0) > 1 and hidden.size(0) * hidden.stride(0) > (1 << 29)):
             hidden = hidden.contiguous()
         if not weight.is_contiguous():
             raise ValueError("weight must be contiguous")

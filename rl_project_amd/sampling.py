@@ -231,16 +231,19 @@ class SamplerPlan:
     is recorded into the graph (the kernels allocate, copy and clear
     nothing)."""
 
-    def __init__(self, logits: torch.Tensor, exact_repeat: bool = False, **kw):
+    def __init__(self, logits: torch.Tensor, exact_repeat: bool = True, **kw):
         want_logprob = kw.pop("return_logprobs", False)
         want_desc = kw.pop("return_desc", False)
         self._call = _Call(logits, flags=0, want_logprob=want_logprob, want_desc=want_desc,
                            finished=kw.pop("finished", None), uniforms=kw.pop("uniforms", None), **kw)
         self._fn = lib().fl_sample
         self._argp = ctypes.byref(self._call.args)
-        # exact_repeat: every launch also enqueues the exact-count repeat for
-        # rows left at FL_ROW_LIMIT (one more kernel; no host synchronisation)
-        self._exact = exact_repeat and logits.dtype != torch.float32
+        # exact_repeat (default): every launch also enqueues the exact-count
+        # repeat for rows left at FL_ROW_LIMIT (one more kernel; no host
+        # synchronisation).  Only 16-bit rows longer than 65535 values can
+        # hold more equal values than a 16-bit counter; a caller that checks
+        # the status itself may turn it off.
+        self._exact = exact_repeat and logits.dtype != torch.float32 and logits.size(-1) > 0xFFFF
 
     def launch(self) -> None:
         rc = self._fn(self._argp, self._call.stream)

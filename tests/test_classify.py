@@ -356,3 +356,72 @@ def test_softcap_saturated_draw_on_the_kernels_values():
     assert tok_far != r.token
     v = C.classify_row(x, p, u, keep, r.token, keep, tok_far, softcap=cap, got_values=far)
     assert v.kind == "MISMATCH", v.details
+
+
+def _kernel16_min_p_top_p(y: torch.Tensor, min_p: float, top_p: float):
+    """CPU model of the 16-bit row kernel's min-p and top-p arithmetic on the
+    distinct values of a row (rl_project_amd/csrc/fl_rows16.hip, the top-k /
+    min-p and top-p phases): e = RN32(exp(y - M)) per value, masses summed
+    exactly in 2^-45 fixed point, r = RN32(1 / RN32(S)); min-p keeps
+    RN(e r) >= RN(RN(r) min_p); over the survivors, r1 = RN32(1 / RN32(S_L)),
+    p = RN(e r1), and sorted position j is removed when
+    RN(RN(RN32(C_j)) - p) >= RN(top_p) with C_j the exact inclusive sum of
+    the p.  Returns (entries kept by min-p, {value: kept members} up to the
+    cut group)."""
+    dt = y.dtype
+    rn = lambda v: float(torch.tensor(float(np.float32(v)), dtype=torch.float32).to(dt).double())
+    vals, counts = torch.unique(y.double(), return_counts=True)
+    vals, counts = vals.flip(0).numpy(), counts.flip(0).numpy()
+    M = vals[0]
+    e = np.array([np.float32(np.exp(np.float64(np.float32(v) - np.float32(M)))) for v in vals], dtype=np.float64)
+    fx = [int(round(v * 2.0 ** 45)) for v in e]
+    S = sum(int(c) * f for c, f in zip(counts, fx)) / 2.0 ** 45
+    r = np.float32(1.0) / np.float32(S)
+    thr = rn(rn(r) * np.float32(min_p))
+    L = next((i for i, v in enumerate(e) if rn(np.float32(v) * r) < thr), len(e))
+    SL = sum(int(c) * f for c, f in zip(counts[:L], fx[:L])) / 2.0 ** 45
+    r1 = np.float32(1.0) / np.float32(SL)
+    t = rn(top_p)
+    c, kept = 0.0, {}
+    for i in range(L):
+        p = rn(np.float32(e[i]) * r1)
+        for j in range(int(counts[i])):
+            c += p
+            if rn(rn(np.float32(c)) - p) >= t:
+                if j:
+                    kept[float(vals[i])] = j
+                return L, kept
+        kept[float(vals[i])] = int(counts[i])
+    return L, kept
+
+
+def test_top_p_cut_on_the_kernels_open_min_p_survivors_f16():
+    """A float16 row of the sampling sweep (seed 71183, row 7: V=151936,
+    soft-cap 5, T 0.7, min-p 0.3, top-p 0.5) whose min-p boundary value lies
+    0.0012 float16-subnormal units from a rounding midpoint: the kernel rounds
+    it down and removes its 65 members, torch's float16 softmax rounds it up
+    and keeps them.  The survivor mass differs, 33 subnormal probabilities move
+    by one unit, and the top-p cut inside a tied group of 535 keeps 276 members
+    (kernel, as the model of its arithmetic reproduces) against 281 (oracle).
+    The classifier judges the cut on the survivor set the kernel used: 276 is
+    NEAR, its neighbours 275 and 277 stay MISMATCH."""
+    from tests.helpers import sweep_case
+
+    w, _ = sweep_case(71183)
+    b = 7
+    x = w.logits[b]
+    assert x.dtype == torch.float16 and x.numel() == 151936 and w.softcap == 5.0
+    p = O.RowParams(float(w.temperature[b]), int(w.top_k[b]), float(w.top_p[b]), float(w.min_p[b]), 1.0, [], [])
+    assert (p.top_k, p.top_p) == (0, 0.5) and abs(p.min_p - 0.3) < 1e-7
+    r, keep, y = _oracle(x, p, float(w.uniforms[b]), softcap=w.softcap)
+    y_cut = 7.04296875
+    grp = torch.nonzero(y == y_cut).flatten()
+    assert grp.numel() == 535 and int(keep[grp].sum()) == 281
+    L, kept = _kernel16_min_p_top_p(y, p.min_p, p.top_p)
+    assert kept[y_cut] == 276
+    # the kernel's mask: every value above the cut group, its 276 lowest indices
+    for n, kind in ((276, "NEAR"), (275, "MISMATCH"), (277, "MISMATCH"), (281, "EXACT")):
+        gk = y > y_cut
+        gk[grp[:n]] = True
+        v = _kind(x, p, float(w.uniforms[b]), keep, r.token, gk, None, softcap=w.softcap)
+        assert v.kind == kind, (n, v.kind, v.details[-2:])

@@ -6,6 +6,7 @@ sample like their contiguous copy; a soft-cap whose x / cap spans both
 branches of the kernels' tanh; and float32 rows saturated by the soft-cap,
 whose draws fall among thousands of values at the cap."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -156,3 +157,21 @@ def test_float32_draws_among_values_at_the_softcap():
     summ, verdicts = classify_workload(w, out.tokens.cpu(), unpack_mask(mask, V), got_values=filt.cpu())
     print(f"   {summ}", flush=True)
     assert summ["MISMATCH"] == 0, [(b, v.details) for b, v in enumerate(verdicts) if not v.ok][:4]
+
+
+def test_softcap_tanh_never_decreases_across_its_switch():
+    """The kernels' tanh is an odd polynomial below |z| = 0.625 and tanhf
+    above, floored at the polynomial's last value; the float32 two-read path
+    bins soft-capped values by a monotone order, so it must never decrease.
+    With cap 1 (x * (1 / 1) and * 1 exact) the filtered values are fl_tanh(x)
+    itself: every float within 4096 units of +-0.625 and windows deep in the
+    tanhf branch come back in non-decreasing order, and within 2 units of
+    float64 tanh."""
+    c = torch.tensor([0.625, 1.0, 2.0, 4.5, 9.0], dtype=torch.float32).view(torch.int32)
+    win = torch.cat([torch.arange(int(b) - 4096, int(b) + 4096, dtype=torch.int32) for b in c]).view(torch.float32)
+    x = torch.sort(torch.cat([win, -win])).values
+    out = filtered_outputs(x[None].cuda(), temperature=1.0, softcap=1.0)[0][0].cpu()
+    assert bool((out[1:] >= out[:-1]).all()), int(torch.nonzero(out[1:] < out[:-1])[0])
+    ref = torch.tanh(x.double())
+    ulp = torch.from_numpy(np.spacing(np.abs(ref.float().numpy()))).double()
+    assert float(((out.double() - ref).abs() / ulp).max()) <= 2.0

@@ -80,3 +80,40 @@ def test_batched_sampler_slots_release_and_state_in_place():
     ptr = a.history.data_ptr()
     a.step(torch.randn(6, V, device="cuda"), uniforms=torch.rand(6, device="cuda"))
     assert a.history.data_ptr() == ptr
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("by_slots", [False, True])
+def test_batched_sampler_stop_token_joins_history(dtype, by_slots):
+    """A row that samples a stop id appends that id and then stops: the
+    reference appends the token before its stop check (inference/engine.py:
+    122-127).  The kernel updates the finished flags in place, so it must read
+    a row's previous flag before writing the new one."""
+    V, EOS, STOP = 4096, 7, 11
+    bs = BatchedSampler(4, 64, V, "cuda", eos_token_id=EOS)
+    greedy = SamplingParams(temperature=0.0, top_k=0, repetition_penalty=1.0, stop_token_ids=[STOP])
+    prompts = [[1, 2, 3], [4, 5], [6], [8, 9, 10, 12]]
+    for s, pr in enumerate(prompts):
+        bs.admit(s, greedy, pr)
+    wins = [EOS, STOP, 100, 200]           # the argmax of each row in the first step
+    x = torch.randn(4, V, generator=torch.Generator().manual_seed(1)).clamp(-3, 3)
+    for b, t in enumerate(wins):
+        x[b, t] = 10.0
+    x = x.to(dtype).cuda()
+    u = torch.full((4,), 0.5, device="cuda")
+    sel = torch.arange(4, device="cuda")
+    out = bs.step(x, uniforms=u, slots=sel) if by_slots else bs.step(x, uniforms=u)
+    assert out.tokens.cpu().tolist() == wins
+    assert out.finished.cpu().tolist() == [True, True, False, False]
+    assert out.status.cpu().tolist() == [0, 0, 0, 0]
+    for b in range(4):
+        assert bs.history_of(b) == prompts[b] + [wins[b]], b
+    # the next step: finished rows still sample but append nothing
+    x2 = x.clone()
+    x2[:, 300] = 20.0
+    bs.step(x2, uniforms=u, slots=sel) if by_slots else bs.step(x2, uniforms=u)
+    assert bs.history_of(0) == prompts[0] + [EOS]
+    assert bs.history_of(1) == prompts[1] + [STOP]
+    assert bs.history_of(2) == prompts[2] + [100, 300]
+    assert bs.history_of(3) == prompts[3] + [200, 300]
+    assert bs.finished.cpu().tolist()[:4] == [True, True, False, False]

@@ -215,3 +215,26 @@ def test_argument_errors():
         LmHeadPlan(h[:, :128], w)
     with pytest.raises(ValueError):   # dim not a multiple of 64
         LmHeadPlan(h[:, :100].contiguous(), w[:, :100].contiguous()).launch()
+
+
+def test_last_position_view_of_prefill_states():
+    """The reference takes the last position of the [B, T, D] hidden states
+    (model.py:190,201): a strided view whose rows lie T*D apart.  Where the
+    rows span more than the kernels' 32-bit offsets reach, the plan copies the
+    view; tokens and log-probs equal those of the contiguous copy."""
+    B, T, D, V = 17, 8192, 4096, 4099
+    assert B * T * D > (1 << 29)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    states = torch.empty(B, T, D, dtype=torch.bfloat16, device="cuda")
+    states[:, -1, :] = torch.randn(B, D, generator=g, device="cuda").to(torch.bfloat16)
+    W = (torch.randn(V, D, generator=g, device="cuda") * (2.5 / D ** 0.5)).to(torch.bfloat16)
+    u = torch.rand(B, generator=g, device="cuda")
+    kw = dict(temperature=0.8, top_k=20, top_p=0.9, uniforms=u, return_logprobs=True)
+    view = states[:, -1, :]
+    assert view.stride(0) == T * D
+    a = lm_head_sample(view, W, **kw)
+    b = lm_head_sample(view.contiguous(), W, **kw)
+    torch.cuda.synchronize()
+    assert a.tokens.tolist() == b.tokens.tolist()
+    assert torch.equal(a.logprobs, b.logprobs)
+    del states

@@ -1,0 +1,29 @@
+"""Cases of the randomized sampling sweep that once came out MISMATCH,
+rebuilt from their seeds and sampled on the GPU (MI355X)."""
+
+import pytest
+import torch
+
+from tests.helpers import run_sweep_case
+
+pytestmark = pytest.mark.gpu
+
+
+def test_sweep_seed_71183_f16_top_p_after_an_open_min_p_boundary():
+    """float16, V=151936, soft-cap 5 (8 rows).  Row 7's min-p boundary value
+    lies 0.0012 float16-subnormal units from a rounding midpoint; the kernel
+    rounds it down (removing its 65 members) where torch rounds it up, and the
+    top-p cut inside a tied group of 535 then keeps 276 members against the
+    oracle's 281.  Correct on the kernel's survivor set; every row must
+    classify without MISMATCH and row 7 must keep exactly 276."""
+    w, ok_rows, st, summ, verdicts, toks, keep = run_sweep_case(71183)
+    print(f"seed 71183: status {st.tolist()} {summ}", flush=True)
+    assert summ["MISMATCH"] == 0, [v.details[:3] for v in verdicts if not v.ok]
+    assert 7 in ok_rows
+    from oracle import sampler_oracle as O
+
+    b = 7
+    y = O.pre_filter_values(w.logits[b][None], float(w.temperature[b]), 1.0, None, w.softcap)[0]
+    grp = torch.nonzero(y == 7.04296875).flatten()
+    assert grp.numel() == 535
+    assert int(keep[ok_rows.index(b)][grp].sum()) == 276

@@ -3,7 +3,10 @@ polynomial below |z| = 0.625, tanhf above) against double-precision tanh
 (CPU only; the C checker uses the host's fmaf, which rounds as the GPU's FMA
 does).  Over every float32 value in [0, 0.625) it must lie within 0.75 ulp of
 tanh, equal the correctly rounded value for all but 0.1 % of the values, and
-never decrease (the two-read float32 path bins values by a monotone order).
+never decrease (the two-read float32 path bins values by a monotone order):
+each checked value is compared with the polynomial at the next float up, and
+the constant that floors the tanhf branch above 0.625 must be the
+polynomial's value at the largest float below it.
 
 By default every 5th float32 value (~15 s); FL_FULL_TANH_SWEEP=1 checks every
 value (~70 s)."""
@@ -45,3 +48,6 @@ def test_polynomial_tanh_within_an_ulp_and_monotone(tmp_path):
     assert max_err <= 0.75
     assert differ <= checked // 1000
     assert decreases == 0
+    # the floor of the tanhf branch is the polynomial's last value below the switch
+    m = re.search(r"constexpr uint32_t TANH_AT_SWITCH_BITS = (0x[0-9a-fA-F]+)u;", open(DEVICE_H).read())
+    assert m and int(m.group(1), 16) == int(f[9], 16), (f[9], m and m.group(1))

@@ -71,3 +71,31 @@ def test_static_scratch_verify_matches_the_workspace_verify():
         p2.launch()
         torch.cuda.synchronize()
         assert torch.equal(p2.n_accepted, plan.n_accepted) and torch.equal(p2.tokens, plan.tokens)
+
+
+def test_no_alloc_plan_recorded_in_a_graph():
+    """SpecPlan(no_alloc=True).launch() -- two fl_sample launches and
+    fl_spec_verify_static -- recorded into a graph under torch's default
+    (global) capture mode, in which an allocation during capture fails.  Each
+    replay, with the program's own eager launches and synchronisations
+    between replays, equals an eager launch of the same plan."""
+    B, K, V, dtype = 32, 5, 128256, torch.float32
+    plan = _plan(B, K, V, dtype, seed=7, no_alloc=True)
+    plan.launch()       # (outside capture: the first call on a device finds the scratch's address)
+    torch.cuda.synchronize()
+    ref_n, ref_t = plan.n_accepted.clone(), plan.tokens.clone()
+    other = _plan(7, 3, 32000, torch.bfloat16, seed=8, no_alloc=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.launch()
+    torch.cuda.synchronize()
+    for i in range(4):
+        print(f"[no-alloc graph] replay {i}", flush=True)
+        plan.n_accepted.fill_(-1)
+        plan.tokens.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.n_accepted, ref_n) and torch.equal(plan.tokens, ref_t)
+        other.launch()      # eager work on the same scratch between replays
+        torch.cuda.synchronize()
+        assert bool(other.status_ok().all())
