@@ -173,9 +173,9 @@ __device__ __forceinline__ float penalty_val(float x, float rp) {
   return x > 0.0f ? D::rn(x / rp) : D::rn(x * rp);
 }
 
-// x / t correctly rounded, for a t fixed per row and rt = RN(1 / t) (one IEEE
-// division per row).  q0 = x * rt lies within one ulp of x / t; the remainder
-// x - t * q0 is then exact in one FMA, and q0 + remainder * rt rounded once is
+// x / t correctly rounded, for a t fixed per row and rt = recip_rt(t) below.
+// q0 = x * rt lies within one ulp of x / t; the remainder x - t * q0 is then
+// exact in one FMA, and q0 + remainder * rt rounded once is
 // RN(x / t): Markstein's correction (P. Markstein, "Computation of elementary
 // functions on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1),
 // 1990; Theorem 8.10 of Muller et al., Handbook of Floating-Point
@@ -198,12 +198,27 @@ __device__ __forceinline__ float div_rt(float x, float t, float rt) {
   return __builtin_fmaf(r, rt, q0);
 }
 
+// The reciprocal div_rt needs for a divisor t fixed per row: RN(1 / t) for t
+// in [2^-100, 2^100], else 0, which sends every quotient to the division
+// itself (a t near 2^127 has a subnormal reciprocal, too short for the
+// correction).  One IEEE division per row.
+__device__ __forceinline__ float recip_rt(float t) {
+  return (t >= 0x1p-100f && t <= 0x1p100f) ? 1.0f / t : 0.0f;
+}
+
+// repetition penalty with the row's rpr = recip_rt(rp): equal to penalty_val
+// bit for bit, the division as div_rt.
+template <class D>
+__device__ __forceinline__ float penalty_val(float x, float rp, float rpr) {
+  return x > 0.0f ? D::rn(div_rt(x, rp, rpr)) : D::rn(x * rp);
+}
+
 // temperature (sampling.py:33-34).
 template <class D>
 __device__ __forceinline__ float temperature_val(float x, float t) {
   return t > 0.0f ? D::rn(x / t) : x;
 }
-// the same with the row's reciprocal rt = RN(1 / t) (equal bit for bit)
+// the same with the row's rt = recip_rt(t) (equal bit for bit)
 template <class D>
 __device__ __forceinline__ float temperature_val(float x, float t, float rt) {
   return t > 0.0f ? D::rn(div_rt(x, t, rt)) : x;

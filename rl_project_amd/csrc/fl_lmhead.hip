@@ -271,7 +271,7 @@ __device__ __forceinline__ LmRowReg lm_row_load(const fl_lm_head_args& a, int m)
 template <int MR>
 __device__ __forceinline__ void lm_row_store(LmRows<MR>& p, int m, const LmRowReg& r) {
   p.T[m] = r.T;
-  p.RT[m] = r.T > 0.0f ? 1.0f / r.T : 0.0f;
+  p.RT[m] = r.T > 0.0f ? recip_rt(r.T) : 0.0f;
   p.RP[m] = r.RP;
   p.pen[m] = r.pen;
 }
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_thresh(const fl_lm_head_args a, Lm
   // of non-members, of members (a row without a penalty has no members)
   static_assert(NW >= 4, "one wave per threshold");
   if (w >= 4) return;
-  const float T = a.temperature[b], RT = T > 0.0f ? 1.0f / T : 0.0f, cap = a.softcap;
+  const float T = a.temperature[b], RT = T > 0.0f ? recip_rt(T) : 0.0f, cap = a.softcap;
   const bool pen = row_penalised(a, b);
   const float RP = pen ? a.repetition_penalty[b] : 1.0f;
   const bool bad = pen && !(RP > 0.0f && RP <= 3.402823466e38f);
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick(const fl_lm_head_args a, LmWs
   __syncthreads();
   if (status == 0) {
     // each candidate's transformed key (the gemm kept its raw key)
-    const float T = a.temperature[b], RT = T > 0.0f ? 1.0f / T : 0.0f, cap = a.softcap;
+    const float T = a.temperature[b], RT = T > 0.0f ? recip_rt(T) : 0.0f, cap = a.softcap;
     const bool pen = row_penalised(a, b);
     const float RP = pen ? a.repetition_penalty[b] : 1.0f;
     const uint32_t* hb = ws.bits + static_cast<size_t>(b) * ws.bw;

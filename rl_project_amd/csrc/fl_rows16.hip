@@ -409,7 +409,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
   // u outside [0, 1) (or NaN) is clamped into it
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const float CAP = a.softcap;
-  const float RT = T > 0.0f ? 1.0f / T : 0.0f;  // one IEEE division per row (temperature_val)
+  const float RT = T > 0.0f ? recip_rt(T) : 0.0f;  // one IEEE division per row (temperature_val)
   // (H_in is only meaningful with a history: without one it was read from the stand-in array)
   const bool hist_too_long = a.hist_ids != nullptr && H_in > FL_MAX_HISTORY;
   const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;

@@ -111,6 +111,7 @@ struct Shared32 {
       uint64_t acc[NBF + 1];  // two-read bins: packed sums, then exclusive mass prefixes; [NBF]: discard slot
       uint32_t pc[NBF];    // exclusive count prefixes
     };
+    alignas(16) uint32_t tkc[1 << 13];  // top-k path bins (key >> 19)
   };
   uint64_t cand[CAP];  // (key << 32) | ~index, sorted descending
   uint64_t cscan[CAP]; // two-read path: inclusive mass prefix at each candidate
@@ -158,14 +159,15 @@ struct Src {
 // Logit -> filtered value: soft-cap, repetition penalty (history elements),
 // temperature, each rounded to float32 as the reference's tensor ops round.
 struct Xform {
-  float cap, rp, t, rt;  // rt = RN(1 / t) when t > 0
+  float cap, rp, t, rt;  // rt = recip_rt(t) when t > 0
+  float rpr;             // recip_rt(rp)
   bool pen;
   const uint32_t* hbits;
   int nch;
   __device__ __forceinline__ float y(float x, bool hist) const {
     float z = x;
     if (cap > 0.0f) z = softcap_val<F32>(z, cap);
-    if (hist) z = penalty_val<F32>(z, rp);
+    if (hist) z = penalty_val<F32>(z, rp, rpr);
     // + 0.0f turns -0 into +0: the filters compare -0 == +0, so both get one key
     return temperature_val<F32>(z, t, rt) + 0.0f;
   }
@@ -175,7 +177,7 @@ struct Xform {
   __device__ __forceinline__ float yt(float x, bool hist) const {
     float z = x;
     if (cap > 0.0f) z = softcap_val<F32>(z, cap);
-    if (PEN && hist) z = penalty_val<F32>(z, rp);
+    if (PEN && hist) z = penalty_val<F32>(z, rp, rpr);
     if (TDIV) z = div_rt(z, t, rt);
     return z + 0.0f;
   }
@@ -195,7 +197,7 @@ struct Xform {
     for (int e = 0; e < 4; ++e) {
       z[e] = xs[e];
       if (cap > 0.0f) z[e] = softcap_val<F32>(z[e], cap);
-      if (PEN && ((hb >> e) & 1u)) z[e] = penalty_val<F32>(z[e], rp);
+      if (PEN && ((hb >> e) & 1u)) z[e] = penalty_val<F32>(z[e], rp, rpr);
     }
     if constexpr (TDIV) {
       float q0[4];
@@ -544,6 +546,511 @@ struct RowOut {
   uint32_t keep_n;
   int64_t tok;
 };
+
+// ------------------------------------------------------------ top-k path
+// Rows with top-k on (a request's default keeps 50, inference/requests.py:26):
+// every decision of sampling.py:36-61 acts on the top-k survivors, which a
+// histogram finds without the filtered values of the whole row.  The value
+// y = RN(z / t) + 0 (sampling.py:33-34) is a non-decreasing function f of the
+// penalised value z (sampling.py:30), so the K-th largest y is f of the K-th
+// largest z, and only candidates need y:
+//   read 1   s = soft-cap(x) (x without soft-cap) adds one to a TK_NB-bin
+//            histogram on bits 31..TK_SH of its order-preserving key (16 bins
+//            per binade); the row's first 4 * TK_TILE * NT keys stay in
+//            registers
+//   history  each element of the history bitmap moves from the bin of s to
+//            the bin of z = penalty(s)
+//   scan     the bin of the K-th largest z (a descending block scan)
+//   read 2   every element in that bin or above becomes a candidate
+//            (key(z) << 32 | ~index, then key(y)); more than TK_CAND of them,
+//            a K-th value at -inf, or one that rounding could tie with a
+//            value below the bin, leave the row to the two-read path, as do
+//            NaN values
+//   decide   one wave over the sorted candidates at or above the K-th value,
+//            64 at a time: min-p, top-p and the inverse CDF on exact 2^-45
+//            masses fx45(exp(y - M)) -- the multi-pass path's arithmetic,
+//            element by element.
+constexpr int TK_MAX = 1024;            // top-k values this path serves
+constexpr int TK_CAND = RANK_SORT_MAX;  // candidates it sorts and decides
+constexpr int TK_TILE = 8;              // chunks per thread whose keys read 1 keeps in registers
+constexpr int TK_SH = 19;               // bin of a key: key >> TK_SH
+constexpr int TK_NB = 1 << (32 - TK_SH);
+constexpr int TK_BPT = TK_NB / NT;      // bins per thread in the scan
+static_assert(TK_CAND <= NT && TK_BPT * NT == TK_NB && TK_BPT % 4 == 0, "top-k shapes");
+static_assert(sizeof(Shared32::tkc) == TK_NB * 4 && TK_NB * 4 <= NB * 24,
+              "the top-k bins share the level-1 and level-2 bins' memory");
+
+// s: the soft-capped logit, the logit itself without soft-cap
+template <bool SC>
+__device__ __forceinline__ float topk_s(const Xform& X, float x) {
+  return SC ? softcap_val<F32>(x, X.cap) : x;
+}
+// y of a penalised value z, as Xform::yt computes it
+template <bool TDIV>
+__device__ __forceinline__ float topk_y(const Xform& X, float z) {
+  return (TDIV ? div_rt(z, X.t, X.rt) : z) + 0.0f;
+}
+
+// Read 1 of four values (chunk ch): bin counts of their s keys, the keys in k
+// (0 past the row's end), bad set on a NaN (or +inf and -inf together).
+// Returns the largest key.
+template <bool SC>
+__device__ __forceinline__ uint32_t topk_count4(Shared32& sh, const Xform& X, int V, int ch, const float4& q,
+                                                uint32_t (&k)[4], bool& bad) {
+  const float s[4] = {topk_s<SC>(X, q.x), topk_s<SC>(X, q.y), topk_s<SC>(X, q.z), topk_s<SC>(X, q.w)};
+  const float sm = (s[0] + s[1]) + (s[2] + s[3]);
+  if (4 * ch + 3 < V) {
+    bad |= sm != sm;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      k[e] = f32_key(s[e]);
+      atomicAdd(&sh.tkc[k[e] >> TK_SH], 1u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      k[e] = 0u;
+      if (4 * ch + e >= V) continue;
+      bad |= s[e] != s[e];
+      k[e] = f32_key(s[e]);
+      atomicAdd(&sh.tkc[k[e] >> TK_SH], 1u);
+    }
+  }
+  return max(max(k[0], k[1]), max(k[2], k[3]));
+}
+
+// The register tile: chunk u * NT + tid for u < TK_TILE, all loads in flight
+// at once (one memory round trip for rows up to 4 * TK_TILE * NT values),
+// issued before the row's history is read.
+__device__ __forceinline__ void topk_tile_load(const Src& S, float4 (&q)[TK_TILE]) {
+#pragma unroll
+  for (int u = 0; u < TK_TILE; ++u) q[u] = S.chunk(u * NT + threadIdx.x);  // (past the row: 0, the buffer's bound)
+}
+
+// Read 1: the register tile q (keys kept in kt, the largest of chunk u in
+// cmx[u]), then the rest of the row.
+template <bool SC>
+__device__ __forceinline__ void topk_read1(Shared32& sh, const Src& S, const Xform& X, int V,
+                                           const float4 (&q)[TK_TILE], uint32_t (&kt)[TK_TILE][4],
+                                           uint32_t (&cmx)[TK_TILE], bool& bad) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < TK_TILE; ++u) {
+    cmx[u] = topk_count4<SC>(sh, X, V, u * NT + tid, q[u], kt[u], bad);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t k[4];
+      topk_count4<SC>(sh, X, V, c0 + u * NT + tid, q[u], k, bad);
+    }
+  }
+}
+
+// History elements (bits of the bitmap X.hbits; thread t takes words t,
+// t + NT, ...).  The first TK_HP of a thread are prefetched before read 1 and
+// kept in registers (index hi, logit hx, then z key hk); the rest, rare, are
+// loaded again by each pass that needs them.
+constexpr int TK_HP = 4;
+struct TopkHist {
+  int hi[TK_HP];
+  float hx[TK_HP];
+  uint32_t hk[TK_HP];
+  bool more;  // the thread's words hold more than TK_HP elements
+};
+
+__device__ __forceinline__ void topk_hist_prefetch(const Src& S, const Xform& X, int V, TopkHist& h) {
+#pragma unroll
+  for (int j = 0; j < TK_HP; ++j) h.hi[j] = -1;
+  h.more = false;
+  const int nw = (V + 31) >> 5;
+  int n = 0;
+  for (int w = threadIdx.x; w < nw && !h.more; w += NT) {
+    uint32_t bits = X.hbits[w];
+    while (bits) {
+      if (n == TK_HP) {
+        h.more = true;
+        break;
+      }
+      const int i = 32 * w + __ffs(bits) - 1;
+      bits &= bits - 1u;
+#pragma unroll
+      for (int j = 0; j < TK_HP; ++j)
+        if (j == n) h.hi[j] = i;  // (static indices: the slots stay in registers)
+      ++n;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TK_HP; ++j)
+    h.hx[j] = h.hi[j] >= 0 ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(S.rs, 4 * h.hi[j], 0, 0)) : 0.0f;
+}
+
+// The history elements past a thread's first TK_HP: f(i, x) for each.
+template <class F>
+__device__ __forceinline__ void topk_hist_rest(const Src& S, const Xform& X, int V, F&& f) {
+  const int nw = (V + 31) >> 5;
+  int n = 0;
+  for (int w = threadIdx.x; w < nw; w += NT) {
+    uint32_t bits = X.hbits[w];
+    while (bits) {
+      const int i = 32 * w + __ffs(bits) - 1;
+      bits &= bits - 1u;
+      if (n++ < TK_HP) continue;
+      f(i, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(S.rs, 4 * i, 0, 0)));
+    }
+  }
+}
+
+// Each history element moves from the bin of s to the bin of z = penalty(s)
+// (bad set on a NaN z); the z keys of the prefetched ones stay in h.hk.
+template <bool SC>
+__device__ __forceinline__ void topk_hist_move(Shared32& sh, const Src& S, const Xform& X, int V, TopkHist& h,
+                                               bool& bad) {
+  auto move = [&](float x) -> uint32_t {
+    const float s = topk_s<SC>(X, x);
+    const float z = penalty_val<F32>(s, X.rp, X.rpr);
+    bad |= z != z;
+    const uint32_t ks = f32_key(s), kz = f32_key(z);
+    if ((ks >> TK_SH) != (kz >> TK_SH)) {
+      atomicSub(&sh.tkc[ks >> TK_SH], 1u);
+      atomicAdd(&sh.tkc[kz >> TK_SH], 1u);
+    }
+    return kz;
+  };
+#pragma unroll
+  for (int j = 0; j < TK_HP; ++j) h.hk[j] = h.hi[j] >= 0 ? move(h.hx[j]) : 0u;
+  if (h.more) topk_hist_rest(S, X, V, [&](int, float x) { move(x); });
+}
+
+// One slot per candidate: (z key << 32) | ~index, z keys turned into y keys
+// before the sort.  A wave's candidates take one atomic: lane l writes its c
+// candidates from the wave's base plus the candidates of lanes below l.
+__device__ __forceinline__ uint32_t topk_slots(Shared32& sh, uint32_t c) {
+  const uint32_t incl = wave_incl_scan(c);
+  const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), WAVE - 1));
+  uint32_t base = 0;
+  if (tot) {
+    if ((threadIdx.x & (WAVE - 1)) == WAVE - 1) base = atomicAdd(&sh.ncand, tot);
+    base = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(base), WAVE - 1));
+  }
+  return base + incl - c;
+}
+__device__ __forceinline__ void topk_put(Shared32& sh, uint32_t& pos, uint32_t kz, int i) {
+  if (pos < static_cast<uint32_t>(CAP))
+    sh.cand[pos] = (static_cast<uint64_t>(kz) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(i));
+  ++pos;
+}
+
+// Read 2: the elements in bin kbin or above (kbin > 0: the zero keys past the
+// row stay out), history elements taken from their own list.
+template <bool SC>
+__device__ __forceinline__ void topk_read2(Shared32& sh, const Src& S, const Xform& X, int V,
+                                           const uint32_t (&kt)[TK_TILE][4], const uint32_t (&cmx)[TK_TILE],
+                                           const TopkHist& h, uint32_t kbin) {
+  const int tid = threadIdx.x;
+  {
+    // the tile: bit 4u + e of m for chunk u, element e (chunks without a
+    // candidate in the whole wave skipped)
+    uint32_t m = 0;
+#pragma unroll
+    for (int u = 0; u < TK_TILE; ++u) {
+      if (__ballot((cmx[u] >> TK_SH) >= kbin)) {
+        uint32_t mu = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mu |= ((kt[u][e] >> TK_SH) >= kbin ? 1u : 0u) << e;
+        if (mu) mu &= ~X.nibble(u * NT + tid);
+        m |= mu << (4 * u);
+      }
+    }
+    uint32_t pos = topk_slots(sh, static_cast<uint32_t>(__popc(m)));
+#pragma unroll
+    for (int u = 0; u < TK_TILE; ++u) {
+      if ((m >> (4 * u)) & 0xFu) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((m >> (4 * u + e)) & 1u) topk_put(sh, pos, kt[u][e], 4 * (u * NT + tid) + e);
+      }
+    }
+  }
+  for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ch = c0 + u * NT + tid;
+      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+      uint32_t k[4], m = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        k[e] = f32_key(topk_s<SC>(X, xs[e]));
+        m |= (4 * ch + e < V && (k[e] >> TK_SH) >= kbin ? 1u : 0u) << e;
+      }
+      if (m) m &= ~X.nibble(ch);
+      if (__ballot(m != 0u)) {
+        uint32_t pos = topk_slots(sh, static_cast<uint32_t>(__popc(m)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((m >> e) & 1u) topk_put(sh, pos, k[e], 4 * ch + e);
+      }
+    }
+  }
+  if (X.pen) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < TK_HP; ++j) m |= (h.hi[j] >= 0 && (h.hk[j] >> TK_SH) >= kbin ? 1u : 0u) << j;
+    if (__ballot(m != 0u)) {
+      uint32_t pos = topk_slots(sh, static_cast<uint32_t>(__popc(m)));
+#pragma unroll
+      for (int j = 0; j < TK_HP; ++j)
+        if ((m >> j) & 1u) topk_put(sh, pos, h.hk[j], h.hi[j]);
+    }
+    if (h.more)
+      topk_hist_rest(S, X, V, [&](int i, float x) {
+        const uint32_t kz = f32_key(penalty_val<F32>(topk_s<SC>(X, x), X.rp, X.rpr));
+        if ((kz >> TK_SH) >= kbin) {
+          uint32_t pos = atomicAdd(&sh.ncand, 1u);
+          topk_put(sh, pos, kz, i);
+        }
+      });
+  }
+}
+
+// Descending order of buf[0, n), n <= TK_CAND, entries distinct and nonzero:
+// each entry goes to its rank, the number of entries greater than it, counted
+// by every wave -- the waves holding an entry each take one slice of the
+// others (rank: n counters, tmp: n entries of scratch).
+__device__ void topk_sort(uint64_t* buf, uint64_t* tmp, uint32_t* rank, int n) {
+  const int t = threadIdx.x;
+  if (t < n) rank[t] = 0;
+  __syncthreads();
+  const int nw = (n + WAVE - 1) / WAVE;  // waves' worth of entries
+  const int w = t / WAVE;
+  if (nw > 0 && w < (NWAVE / nw) * nw) {
+    const int i = (w % nw) * WAVE + (t & (WAVE - 1));
+    const int np = NWAVE / nw, p = w / nw;
+    const int j0 = (n * p) / np, j1 = (n * (p + 1)) / np;
+    const uint64_t mine = i < n ? buf[i] : ~0ull;
+    uint32_t r = 0;
+    int j = j0;
+    for (; j + 4 <= j1; j += 4) {
+      const uint64_t a0 = buf[j], a1 = buf[j + 1], a2 = buf[j + 2], a3 = buf[j + 3];
+      r += (a0 > mine ? 1u : 0u) + (a1 > mine ? 1u : 0u) + (a2 > mine ? 1u : 0u) + (a3 > mine ? 1u : 0u);
+    }
+    for (; j < j1; ++j) r += buf[j] > mine ? 1u : 0u;
+    if (i < n && r) atomicAdd(&rank[i], r);
+  }
+  __syncthreads();
+  if (t < n) tmp[rank[t]] = buf[t];
+  __syncthreads();
+  if (t < n) buf[t] = tmp[t];
+  __syncthreads();
+}
+
+// The top-k path.  Returns false, with nothing decided, when the row needs
+// another path.  Called by all threads (block-uniform control flow).
+// The bins, zeroed (and the candidate count) before the first barrier of a
+// top-k row.
+__device__ __forceinline__ void topk_init(Shared32& sh) {
+  uint4* z4 = reinterpret_cast<uint4*>(sh.tkc);
+  for (int i = threadIdx.x; i < TK_NB / 4; i += NT) z4[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (threadIdx.x == 0) {
+    sh.ncand = 0;
+    sh.pick_bin = -1;
+  }
+}
+
+// The top-k path, after topk_init and topk_tile_load (q) and a barrier.
+// Returns false, with nothing decided, when the row needs another path.
+// Called by all threads (block-uniform control flow).
+__device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xform& X, const RowCfg& R, RowOut& o,
+                                          const float4 (&q)[TK_TILE]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (WAVE - 1);
+  const int V = R.V, K = R.K;
+  if (sh.status != 0) return false;  // (rows with an error status: the two-read path reports them)
+  const bool sc = X.cap > 0.0f, tdiv = X.t > 0.0f;
+  TopkHist h;
+  if (X.pen) topk_hist_prefetch(S, X, V, h);
+  uint32_t kt[TK_TILE][4], cmx[TK_TILE];
+  bool bad = false;
+  if (sc) topk_read1<true>(sh, S, X, V, q, kt, cmx, bad);
+  else topk_read1<false>(sh, S, X, V, q, kt, cmx, bad);
+  FL_MARK(1);
+  if (X.pen) {
+    __syncthreads();  // (every add of read 1 before the moves)
+    FL_MARK(10);
+    if (sc) topk_hist_move<true>(sh, S, X, V, h, bad);
+    else topk_hist_move<false>(sh, S, X, V, h, bad);
+  }
+  if (block_reduce<uint32_t>(bad ? 1u : 0u, OpMax(), sh.redu) != 0u) return false;
+  FL_MARK(11);
+
+  // ---------------------------------------------- bin of the K-th largest value
+  // (thread t takes bins TK_NB - 1 - TK_BPT t down to TK_NB - TK_BPT (t + 1):
+  // the scan runs down the values)
+  {
+    const int b0 = TK_NB - TK_BPT * (tid + 1);
+    uint32_t c[TK_BPT];
+#pragma unroll
+    for (int q = 0; q < TK_BPT / 4; ++q) {
+      const uint4 v = reinterpret_cast<const uint4*>(sh.tkc + b0)[q];
+      c[4 * q] = v.x;
+      c[4 * q + 1] = v.y;
+      c[4 * q + 2] = v.z;
+      c[4 * q + 3] = v.w;
+    }
+    uint32_t sum = 0;
+#pragma unroll
+    for (int q = 0; q < TK_BPT; ++q) sum += c[q];
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<uint32_t>(sum, sh.redu, &tot);
+    const uint32_t k = static_cast<uint32_t>(K);
+    if (ex < k && ex + sum >= k) {
+      uint32_t run = ex;
+      bool done = false;
+#pragma unroll
+      for (int q = TK_BPT - 1; q >= 0; --q) {
+        if (!done && run + c[q] >= k) {
+          sh.pick_bin = b0 + q;
+          sh.pick_n = run + c[q];  // members of that bin and above
+          done = true;
+        }
+        run += c[q];
+      }
+    }
+  }
+  __syncthreads();
+  const int kbin = sh.pick_bin;
+  const uint32_t nc = sh.pick_n;
+  // (a K-th value at -inf keeps every finite value: not a few candidates)
+  if (kbin <= static_cast<int>(KEY_NEG_INF >> TK_SH) || nc > static_cast<uint32_t>(TK_CAND)) return false;
+  FL_MARK(2);
+
+  // ---------------------------------------------- read 2: the candidates
+  if (sc) topk_read2<true>(sh, S, X, V, kt, cmx, h, static_cast<uint32_t>(kbin));
+  else topk_read2<false>(sh, S, X, V, kt, cmx, h, static_cast<uint32_t>(kbin));
+  __syncthreads();
+  const int n = static_cast<int>(sh.ncand);
+  if (n != static_cast<int>(nc)) return false;  // (cannot happen: the reads compute the same values)
+  // z keys -> y keys (y = f(z), f non-decreasing: the order of the candidates stays)
+  if (tid < n) {
+    const uint64_t c = sh.cand[tid];
+    const float z = f32_of_key(static_cast<uint32_t>(c >> 32));
+    const float y = tdiv ? topk_y<true>(X, z) : topk_y<false>(X, z);
+    sh.cand[tid] = (static_cast<uint64_t>(f32_key(y)) << 32) | static_cast<uint32_t>(c);
+  }
+  FL_MARK(3);
+  topk_sort(sh.cand, sh.cscan, reinterpret_cast<uint32_t*>(sh.cscan + TK_CAND), n);
+  FL_MARK(4);
+  // The K-th largest y and the largest: a K-th value at -inf, or one that an
+  // element below the bin could round to (f of the largest z below the bin
+  // equals it), leaves the row to the two-read path; a maximum at +inf is the
+  // row's status.
+  const uint32_t kmx = static_cast<uint32_t>(sh.cand[0] >> 32);
+  const uint32_t tau = static_cast<uint32_t>(sh.cand[K - 1] >> 32);  // the K-th largest value; ties stay
+  if (kmx < KEY_POS_INF) {
+    const float zb = f32_of_key((static_cast<uint32_t>(kbin) << TK_SH) - 1u);
+    const uint32_t kb = f32_key(tdiv ? topk_y<true>(X, zb) : topk_y<false>(X, zb));
+    if (tau <= KEY_NEG_INF || kb >= tau) return false;
+  }
+  o.kmax = kmx;
+  o.status = kmx >= KEY_POS_INF ? FL_ROW_INF : 0;
+  o.tau = KEY_MIN_FINITE;
+  o.CK = static_cast<uint64_t>(KEY_MIN_FINITE) << 32;
+  o.keep_mass = 0;
+  o.keep_n = 0;
+  o.tok = -1;
+  if (o.status != 0) return true;
+
+  // ---------------------------------------------- decisions (wave 0)
+  // Kept by top-k: the nt candidates at or above tau, a prefix of the sorted
+  // ones; min-p keeps a prefix of those (exp(y - M) falls along the order).
+  // sh.cscan[i]: the inclusive mass prefix at sorted position i.
+  if (tid < WAVE) {
+    const float M = f32_of_key(kmx);
+    const bool mp_on = R.MP > 0.0f, tp_on = R.TP > 0.0f && R.TP < 1.0f;
+    int nt = K;
+    while (nt < n && static_cast<uint32_t>(sh.cand[nt] >> 32) >= tau) ++nt;  // (ties with the K-th value)
+    uint32_t keep_n = 0;
+    uint64_t keep_mass = 0;
+    for (int r0 = 0; r0 < nt; r0 += WAVE) {
+      const int i = r0 + lane;
+      const bool valid = i < nt;
+      const float e = valid ? expf(f32_of_key(static_cast<uint32_t>(sh.cand[i] >> 32)) - M) : 0.0f;
+      const bool kept = valid && (!mp_on || e >= R.MP);  // (sampling.py:40-43 with the common 1/S cancelled)
+      const uint64_t f = kept ? fx45(e) : 0ull;
+      const uint64_t incl = keep_mass + wave_incl_scan(f);
+      if (valid) sh.cscan[i] = incl;
+      keep_n += static_cast<uint32_t>(__popcll(__ballot(kept)));
+      keep_mass = readlane64(incl, WAVE - 1);
+    }
+    __builtin_amdgcn_wave_barrier();  // (the prefixes above before the reads below)
+    // (the first sorted position i < keep_n where pred(i) holds, or -1)
+    auto first = [&](auto pred) -> int {
+      for (int r0 = 0; r0 < static_cast<int>(keep_n); r0 += WAVE) {
+        const int i = r0 + lane;
+        const uint64_t m = __ballot(i < static_cast<int>(keep_n) && pred(i));
+        if (m) return r0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+      }
+      return -1;
+    };
+    bool cut = false;
+    if (tp_on && keep_n > 0) {
+      // first kept position whose exclusive mass reaches ceil(top_p * kept mass)
+      const uint64_t thr = static_cast<uint64_t>(ceil(static_cast<double>(R.TP) * static_cast<double>(keep_mass)));
+      const int p = first([&](int i) { return (i == 0 ? 0ull : sh.cscan[i - 1]) >= thr; });
+      if (p >= 0) {
+        keep_n = static_cast<uint32_t>(p);
+        keep_mass = p == 0 ? 0ull : sh.cscan[p - 1];
+        cut = true;
+      }
+    }
+    int64_t tok = -1;
+    uint64_t CK = static_cast<uint64_t>(KEY_MIN_FINITE) << 32;
+    uint32_t tau_out = KEY_MIN_FINITE;
+    int32_t st = 0;
+    if (keep_n == 0) {
+      st |= FL_ROW_ALL_MASKED;
+    } else {
+      const uint64_t last = sh.cand[keep_n - 1];
+      tau_out = static_cast<uint32_t>(last >> 32);
+      CK = cut ? last : static_cast<uint64_t>(tau_out) << 32;
+      if (R.select) {
+        int is = 0;
+        if (R.T > 0.0f) {
+          // inverse CDF: first kept candidate whose inclusive mass exceeds
+          // floor(u * kept mass) (the last kept one when none does)
+          const uint64_t target = static_cast<uint64_t>(floor(static_cast<double>(R.U) * static_cast<double>(keep_mass)));
+          is = first([&](int i) { return sh.cscan[i] > target; });
+          if (is < 0) is = static_cast<int>(keep_n) - 1;
+        }
+        tok = static_cast<int64_t>(~static_cast<uint32_t>(sh.cand[is]));
+      }
+    }
+    if (lane == 0) {
+      sh.bcast_u = static_cast<uint32_t>(st);
+      sh.fkey[0] = tau_out;
+      sh.fck = CK;
+      sh.fmass_out = keep_mass;
+      sh.pick_n = keep_n;
+      sh.ftok = tok;
+    }
+  }
+  __syncthreads();
+  o.status = static_cast<int32_t>(sh.bcast_u);
+  o.tau = sh.fkey[0];
+  o.CK = sh.fck;
+  o.keep_mass = sh.fmass_out;
+  o.keep_n = sh.pick_n;
+  o.tok = sh.ftok;
+  FL_MARK(7);
+  return true;
+}
 
 // Read 1 of the two-read path: anchor the bins on the largest value among the
 // first 4 chunks per thread, then add every element to its bin.  Returns false
@@ -1114,6 +1621,19 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const int nch = (V + 3) >> 2;
   FL_MARK(0);
 
+  Src S;
+  S.rs = row_rsrc(row, 4u * static_cast<uint32_t>(V));
+  S.V = V;
+  S.nfull = V >> 2;
+  S.aligned = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+  // top-k rows: the first loads of the row go out before the history is read
+  const bool topk_first = K > 0 && K < V && K <= TK_MAX;
+  float4 q[TK_TILE];
+  if (topk_first) {
+    topk_tile_load(S, q);
+    topk_init(sh);
+  }
+
   if (tid == 0) {
     sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
     sh.result = -1;
@@ -1133,16 +1653,12 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   }
   __syncthreads();
 
-  Src S;
-  S.rs = row_rsrc(row, 4u * static_cast<uint32_t>(V));
-  S.V = V;
-  S.nfull = V >> 2;
-  S.aligned = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
   Xform X;
   X.cap = a.softcap;
   X.rp = RP;
   X.t = T == 1.0f ? 0.0f : T;  // x / 1 == x exactly: skip the division
-  X.rt = X.t > 0.0f ? 1.0f / X.t : 0.0f;
+  X.rt = X.t > 0.0f ? recip_rt(X.t) : 0.0f;
+  X.rpr = recip_rt(RP);
   X.pen = pen;
   X.hbits = hbits_dyn;
   X.nch = nch;
@@ -1156,7 +1672,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   R.U = U;
   R.select = select;
   RowOut o;
-  if (!two_read(sh, S, X, R, o)) {
+  if (!(topk_first && topk_path(sh, S, X, R, o, q)) && !two_read(sh, S, X, R, o)) {
   // ------------------------------------------------ first read: max, NaN
   uint32_t kmax = 0;
   int nan = 0;
@@ -1579,7 +2095,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
     }
   }
   float y_sel = 0.0f;
-  if (tid == 0 && status == 0 && tok >= 0) {
+  if (tid == 0 && status == 0 && tok >= 0 && a.out_logprob) {
     const int i = static_cast<int>(tok);
     y_sel = X.y(row[i], (X.nibble(i >> 2) >> (i & 3)) & 1u);
   }

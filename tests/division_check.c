@@ -1,6 +1,7 @@
 /* Markstein-corrected division against IEEE division (the kernels' div_rt).
  *
- *   q0 = x * rt, r = fma(-t, q0, x), q1 = fma(r, rt, q0),  rt = RN(1 / t)
+ *   q0 = x * rt, r = fma(-t, q0, x), q1 = fma(r, rt, q0),
+ *   rt = recip_rt(t) = RN(1 / t) for t in [2^-100, 2^100], else 0
  *
  * must equal RN(x / t) wherever the guard of div_rt lets it through
  * (|x|, |q0| in [2^-100, 2^100]).  RN(x / t) is computed in double and rounded
@@ -16,6 +17,8 @@
 
 static float f_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t u_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+static float recip_rt(float t) { return (t >= 0x1p-100f && t <= 0x1p100f) ? 1.0f / t : 0.0f; }
 
 static int same(float x, float t, float rt) {
   const float q0 = x * rt;
@@ -38,7 +41,7 @@ int main(int argc, char** argv) {
   const long nf = argc > 3 ? atol(argv[3]) : 2;
   long n = 0, bad = 0;
   for (long i = 0; i < nb; ++i) {
-    const float t = divisor(i), rt = 1.0f / t;
+    const float t = divisor(i), rt = recip_rt(t);
     for (uint32_t p = 0; p < 65536; ++p) {
       const float x = f_of(p << 16);
       if (!isfinite(x)) continue;
@@ -47,10 +50,31 @@ int main(int argc, char** argv) {
     }
   }
   printf("bf16 %ld %ld\n", n, bad);
+  /* divisors over the whole float range: 2^e times 5 mantissas, e in
+     [-127, 127], and the neighbours of the recip_rt bounds */
+  long nw = 0, badw = 0;
+  const float ms[] = {1.0f, 1.0000001f, 1.3f, 1.7182818f, 1.9999999f};
+  for (int e = -127; e <= 128; ++e) {
+    for (int k = 0; k < 6; ++k) {
+      float t;
+      if (e == 128) t = k < 3 ? f_of(u_of(0x1p-100f) + (uint32_t)k - 1u) : f_of(u_of(0x1p100f) + (uint32_t)k - 4u);
+      else if (k < 5) t = ldexpf(ms[k], e);
+      else t = f_of(u_of(ldexpf(1.0f, e)) - 1u);
+      if (!(t > 0.0f) || !isfinite(t)) continue;
+      const float rt = recip_rt(t);
+      for (uint32_t p = 0; p < 65536; ++p) {
+        const float x = f_of(p << 16);
+        if (!isfinite(x)) continue;
+        ++nw;
+        if (!same(x, t, rt)) { if (badw < 5) printf("bad wide x=%a t=%a\n", x, t); ++badw; }
+      }
+    }
+  }
+  printf("wide %ld %ld\n", nw, badw);
   const float ts[] = {0.8f, 0.7f, 1.3f, 0.1f, 1.5f, 0.123456f, 3.0f, 0.99999994f};
   long n32 = 0, bad32 = 0;
   for (long j = 0; j < nf && j < 8; ++j) {
-    const float t = ts[j], rt = 1.0f / t;
+    const float t = ts[j], rt = recip_rt(t);
     for (uint64_t u = (uint64_t)j; u < (1ull << 32); u += (uint64_t)stride) {
       const float x = f_of((uint32_t)u);
       if (!isfinite(x)) continue;
@@ -59,5 +83,5 @@ int main(int argc, char** argv) {
     }
   }
   printf("f32 %ld %ld\n", n32, bad32);
-  return (bad || bad32) ? 1 : 0;
+  return (bad || bad32 || badw) ? 1 : 0;
 }
