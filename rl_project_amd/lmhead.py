@@ -12,6 +12,12 @@ Rows the fused kernels cannot decide (top-k off or above 64, more than 4096
 values tied above the threshold) report ``FL_ROW_LIMIT``; ``lm_head_sample``
 then samples them with ``fl_sample`` over the logits the GEMM computed (the
 same GEMM run with its logits output on).
+
+On MI355X the fused step is slower than ``torch.nn.functional.linear``
+(hipBLASLt) followed by ``fl_sample`` at every batch size measured (B = 1 to
+64 at D = 4096, V = 128256: 230-268 us against 220-243 us).  So
+``lm_head_sample`` takes the unfused path unless asked for the fused one
+(``fused=True``), which callers that cannot hold the ``[B, V]`` logits use.
 """
 
 from __future__ import annotations
@@ -25,6 +31,14 @@ import torch
 from . import _lib
 from ._lib import LmHeadArgs, check, lib, ptr
 from .sampling import PerRow, _history_tensor, _per_row, _raise_on_status, sample_tokens
+
+
+def fused_is_faster(batch: int, dim: int, vocab: int) -> bool:
+    """Whether the fused kernels beat ``linear`` + ``fl_sample`` for this shape:
+    the crossover measured on MI355X.  At D = 4096, V = 128256 and every B from
+    1 to 64 the unfused path was faster (by 10 us at B = 1, 25 us at B = 64),
+    so no measured shape picks the fused path."""
+    return False
 
 
 @dataclass
@@ -119,14 +133,32 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, *, temperature: P
                    top_p: PerRow = None, min_p: PerRow = None, repetition_penalty: PerRow = None, history=None,
                    softcap: float = 0.0, uniforms: Optional[torch.Tensor] = None,
                    generator: Optional[torch.Generator] = None, return_logprobs: bool = False,
-                   return_logits: bool = False, check_status: bool = True) -> LmHeadOutput:
+                   return_logits: bool = False, check_status: bool = True,
+                   fused: Optional[bool] = None) -> LmHeadOutput:
     """One decode step's ``lm_head`` and sampling (one token per row).
 
-    Rows the fused kernels leave at ``FL_ROW_LIMIT`` are sampled by
-    ``fl_sample`` over the GEMM's logits, with the same uniforms; any other
-    row status raises ``SamplingError`` (unless ``check_status`` is off).
-    Batches above 64 rows run in groups of 64."""
+    ``fused`` None picks the faster path for the shape (``fused_is_faster``):
+    today always ``torch.nn.functional.linear`` followed by ``sample_tokens``,
+    the reference's own two steps (``model.py:190,201``, ``sampling.py:16-61``).
+    ``fused=True`` runs the fused kernels: rows they leave at ``FL_ROW_LIMIT``
+    are sampled by ``fl_sample`` over the GEMM's logits, with the same
+    uniforms, and batches above 64 rows run in groups of 64.  Any other row
+    status raises ``SamplingError`` (unless ``check_status`` is off)."""
     B = hidden.size(0)
+    if fused is None:
+        fused = fused_is_faster(B, hidden.size(-1), weight.size(0))
+    if not fused:
+        if hidden.dim() != 2 or weight.dim() != 2 or hidden.size(1) != weight.size(1):
+            raise ValueError(f"hidden [B, D] and weight [V, D] expected, got {tuple(hidden.shape)} and "
+                             f"{tuple(weight.shape)}")
+        if uniforms is None:
+            uniforms = torch.rand(B, device=hidden.device, generator=generator)
+        logits = torch.nn.functional.linear(hidden, weight)
+        out = sample_tokens(logits, temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+                            repetition_penalty=1.0 if repetition_penalty is None else repetition_penalty,
+                            history=history, softcap=softcap, uniforms=uniforms,
+                            return_logprobs=return_logprobs, check_status=check_status)
+        return LmHeadOutput(out.tokens, out.status, out.logprobs, logits if return_logits else None)
     if B > _lib.FL_LM_HEAD_MAX_BATCH:
         dev = hidden.device
         T, K = _per_row(temperature, B, torch.float32, dev, 1.0), _per_row(top_k, B, torch.int32, dev, 0)
@@ -141,7 +173,7 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, *, temperature: P
                                        min_p=MP[s:e], repetition_penalty=RP[s:e],
                                        history=None if hist is None else (hist[s:e], hlen[s:e]), softcap=softcap,
                                        uniforms=U[s:e], return_logprobs=return_logprobs,
-                                       return_logits=return_logits, check_status=check_status))
+                                       return_logits=return_logits, check_status=check_status, fused=True))
         cat = lambda xs: None if xs[0] is None else torch.cat(xs)  # noqa: E731
         return LmHeadOutput(cat([o.tokens for o in outs]), cat([o.status for o in outs]),
                             cat([o.logprobs for o in outs]), cat([o.logits for o in outs]))

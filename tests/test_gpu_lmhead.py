@@ -117,7 +117,7 @@ def test_rows_the_fused_path_cannot_decide():
     torch.cuda.synchronize()
     L = _lib.FL_ROW_LIMIT
     assert plan.status.tolist() == [L, L, 0, L, 0, 0], plan.status.tolist()
-    out = lm_head_sample(h, w, return_logprobs=True, **kd)
+    out = lm_head_sample(h, w, return_logprobs=True, fused=True, **kd)
     ref = sample_tokens(plan.logits, return_logprobs=True, **kd)
     torch.cuda.synchronize()
     assert out.status.tolist() == [0] * B
@@ -161,7 +161,7 @@ def test_penalties_temperatures_and_overflow():
         assert st[b] == rst[b] == 0, (b, st[b], rst[b])
         assert int(plan.tokens[b]) == int(ref.tokens[b]), b
         assert plan.logprob[b].view(torch.int32).item() == ref.logprobs[b].view(torch.int32).item(), b
-    out = lm_head_sample(h, w, return_logprobs=True, check_status=False, **kd)
+    out = lm_head_sample(h, w, return_logprobs=True, check_status=False, fused=True, **kd)
     torch.cuda.synchronize()
     assert out.status.tolist()[:2] + out.status.tolist()[3:] == rst[:2] + rst[3:]
     assert torch.equal(out.tokens[[0, 1, 3, 4, 5, 6, 7]], ref.tokens[[0, 1, 3, 4, 5, 6, 7]])
@@ -173,7 +173,7 @@ def test_batches_above_64_rows_run_in_groups():
     h, w = _operands(B, D, V, seed=11)
     kw = _params(B, V, seed=12)
     kd = {k: v.cuda() for k, v in kw.items()}
-    out = lm_head_sample(h, w, return_logits=True, **kd)
+    out = lm_head_sample(h, w, return_logits=True, fused=True, **kd)
     ref = sample_tokens(out.logits, **kd)
     torch.cuda.synchronize()
     assert torch.equal(out.tokens, ref.tokens)
@@ -199,7 +199,7 @@ def test_random_lm_head_cases(first):
                   history=torch.randint(0, V, (B, rng.choice([1, 32, 300])), generator=g, dtype=torch.int32),
                   uniforms=torch.rand(B, generator=g))
         kd = {k: v.cuda() for k, v in kw.items()}
-        out = lm_head_sample(h, w, softcap=cap, return_logprobs=True, return_logits=True, **kd)
+        out = lm_head_sample(h, w, softcap=cap, return_logprobs=True, return_logits=True, fused=True, **kd)
         ref = sample_tokens(out.logits, softcap=cap, return_logprobs=True, **kd)
         torch.cuda.synchronize()
         assert out.status.tolist() == [0] * B
@@ -232,9 +232,32 @@ def test_last_position_view_of_prefill_states():
     kw = dict(temperature=0.8, top_k=20, top_p=0.9, uniforms=u, return_logprobs=True)
     view = states[:, -1, :]
     assert view.stride(0) == T * D
-    a = lm_head_sample(view, W, **kw)
-    b = lm_head_sample(view.contiguous(), W, **kw)
+    a = lm_head_sample(view, W, fused=True, **kw)
+    b = lm_head_sample(view.contiguous(), W, fused=True, **kw)
     torch.cuda.synchronize()
     assert a.tokens.tolist() == b.tokens.tolist()
     assert torch.equal(a.logprobs, b.logprobs)
     del states
+
+
+def test_default_path_is_linear_then_fl_sample():
+    """lm_head_sample without ``fused`` takes the path measured faster on
+    MI355X at every batch size: torch's linear (the reference's lm_head) and
+    then fl_sample, exactly -- and the fused kernels' logits stay within the
+    bf16 rounding of the same products."""
+    B, D, V = 24, 1024, 32000
+    print(f"[lm_head default] B={B} D={D} V={V}", flush=True)
+    h, w = _operands(B, D, V, seed=31)
+    kw = _params(B, V, seed=32)
+    kd = {k: v.cuda() for k, v in kw.items()}
+    out = lm_head_sample(h, w, return_logprobs=True, return_logits=True, **kd)
+    logits = torch.nn.functional.linear(h, w)
+    ref = sample_tokens(logits, return_logprobs=True, **kd)
+    fz = lm_head_sample(h, w, return_logits=True, fused=True, **kd)
+    torch.cuda.synchronize()
+    assert torch.equal(out.logits, logits)
+    assert torch.equal(out.tokens, ref.tokens)
+    assert torch.equal(out.logprobs.view(torch.int32), ref.logprobs.view(torch.int32))
+    _check_logits(h, w, fz.logits)
+    assert float((fz.logits.float() - logits.float()).abs().max()) <= \
+        float(logits.float().abs().max()) * 2.0 ** -7
