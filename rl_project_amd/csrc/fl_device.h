@@ -150,6 +150,31 @@ __device__ __forceinline__ float fl_tanh(float z) {
   return copysignf(a < lo ? lo : a, z);
 }
 
+// fl_tanh of four values with one range test: the polynomial for all four
+// when every |z| is below the switch (a row's logits over a soft-cap nearly
+// always are), else fl_tanh one by one.  Equal to fl_tanh element by element.
+__device__ __forceinline__ void fl_tanh4(float (&z)[4]) {
+  const float m = fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3])));
+  if (m < 0.625f) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = z[e] * z[e];
+      float p = __builtin_fmaf(t, TANH_P[5], TANH_P[4]);
+      p = __builtin_fmaf(t, p, TANH_P[3]);
+      p = __builtin_fmaf(t, p, TANH_P[2]);
+      p = __builtin_fmaf(t, p, TANH_P[1]);
+      p = __builtin_fmaf(t, p, TANH_P[0]);
+      z[e] = __builtin_fmaf(z[e] * t, p, z[e]);
+    }
+  } else {
+    // (the empty volatile asm keeps this a branch: speculated, the tanhf
+    // sequence would run for every chunk)
+    asm volatile("" : "+v"(z[0]));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) z[e] = fl_tanh(z[e]);
+  }
+}
+
 // soft-cap tanh(x / c) * c  (models/attention/causal.py:109-110): three ops.
 template <class D>
 __device__ __forceinline__ float softcap_val(float x, float cap) {
@@ -165,6 +190,17 @@ __device__ __forceinline__ float softcap_val(float x, float cap) {
     const float t = D::rn(fl_tanh(a));
     return D::rn(t * cap);
   }
+}
+
+// The float32 soft-cap of four values, rcap = RN(1 / cap): softcap_val<F32>
+// element by element.
+__device__ __forceinline__ void softcap4_f32(float (&x)[4], float cap, float rcap) {
+  float z[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) z[e] = x[e] * rcap;
+  fl_tanh4(z);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = z[e] * cap;
 }
 
 // repetition penalty on one value (sampling.py:30): x>0 ? x/rp : x*rp.

@@ -154,6 +154,25 @@ struct Src {
     f.w = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 16 * c + 12, 0, 0));
     return f;
   }
+  // chunks c0 + u * NT + tid, u < U.  When all of them are whole chunks of an
+  // aligned row (every iteration of a streaming loop but the last), one
+  // uniform test covers them and each is one 16-byte load; a test per chunk
+  // would put a branch around every load and make the wave wait for all U
+  // loads before it uses the first.
+  template <int U>
+  __device__ __forceinline__ void chunks(int c0, float4 (&q)[U]) const {
+    const int tid = threadIdx.x;
+    if (aligned && c0 + U * NT <= nfull) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint4 v = buf_load16(rs, 16u * static_cast<uint32_t>(c0 + u * NT + tid), 0u);
+        q[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) q[u] = chunk(c0 + u * NT + tid);
+    }
+  }
 };
 
 // Logit -> filtered value: soft-cap, repetition penalty (history elements),
@@ -161,6 +180,7 @@ struct Src {
 struct Xform {
   float cap, rp, t, rt;  // rt = recip_rt(t) when t > 0
   float rpr;             // recip_rt(rp)
+  float rcap;            // RN(1 / cap) when cap > 0
   bool pen;
   const uint32_t* hbits;
   int nch;
@@ -181,24 +201,27 @@ struct Xform {
     if (TDIV) z = div_rt(z, t, rt);
     return z + 0.0f;
   }
-  // yt of the four elements of a chunk (history bits hb).  With TDIV the
-  // range guard of div_rt is taken once for the chunk: when every element
-  // passes it (the usual case) each quotient is Markstein's two FMAs, else
-  // each element takes div_rt.  Equal to yt() bit for bit.
-  template <bool TDIV, bool PEN>
+  // yt of the four elements of a chunk (history bits hb), SC = cap > 0 fixed
+  // at compile time (the soft-cap's tanh range test taken once for the
+  // chunk).  With TDIV the range guard of div_rt is taken once for the
+  // chunk: when every element passes it (the usual case) each quotient is
+  // Markstein's two FMAs, else each element takes div_rt.  Equal to yt() bit
+  // for bit.
+  template <bool TDIV, bool PEN, bool SC>
   __device__ __forceinline__ void yt4(const float (&xs)[4], uint32_t hb, float (&y)[4]) const {
-    if constexpr (!TDIV) {  // (element by element: soft-capped rows interleave better)
+    float z[4] = {xs[0], xs[1], xs[2], xs[3]};
+    if constexpr (SC) softcap4_f32(z, cap, rcap);
+    if constexpr (!TDIV) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = yt<false, PEN>(xs[e], (hb >> e) & 1u);
+      for (int e = 0; e < 4; ++e) {
+        if (PEN && ((hb >> e) & 1u)) z[e] = penalty_val<F32>(z[e], rp, rpr);
+        y[e] = z[e] + 0.0f;
+      }
       return;
     }
-    float z[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      z[e] = xs[e];
-      if (cap > 0.0f) z[e] = softcap_val<F32>(z[e], cap);
+    for (int e = 0; e < 4; ++e)
       if (PEN && ((hb >> e) & 1u)) z[e] = penalty_val<F32>(z[e], rp, rpr);
-    }
     if constexpr (TDIV) {
       float q0[4];
 #pragma unroll
@@ -231,8 +254,7 @@ __device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f, in
   const int nch = X.nch;
   for (int c0 = from; c0 < nch; c0 += 4 * NT) {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+    S.chunks(c0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = c0 + u * NT + tid;
@@ -256,8 +278,7 @@ __device__ __forceinline__ void row_pass_raw(const Src& S, const Xform& X, F&& f
   const int nch = X.nch;
   for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+    S.chunks(c0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = c0 + u * NT + tid;
@@ -623,8 +644,7 @@ __device__ __forceinline__ uint32_t topk_count4(Shared32& sh, const Xform& X, in
 // at once (one memory round trip for rows up to 4 * TK_TILE * NT values),
 // issued before the row's history is read.
 __device__ __forceinline__ void topk_tile_load(const Src& S, float4 (&q)[TK_TILE]) {
-#pragma unroll
-  for (int u = 0; u < TK_TILE; ++u) q[u] = S.chunk(u * NT + threadIdx.x);  // (past the row: 0, the buffer's bound)
+  S.chunks(0, q);  // (past the row: 0, the buffer's bound)
 }
 
 // Read 1: the register tile q (keys kept in kt, the largest of chunk u in
@@ -641,8 +661,7 @@ __device__ __forceinline__ void topk_read1(Shared32& sh, const Src& S, const Xfo
   }
   for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+    S.chunks(c0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       uint32_t k[4];
@@ -778,8 +797,7 @@ __device__ __forceinline__ void topk_read2(Shared32& sh, const Src& S, const Xfo
   }
   for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+    S.chunks(c0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int ch = c0 + u * NT + tid;
@@ -1055,7 +1073,7 @@ __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xfor
 // Read 1 of the two-read path: anchor the bins on the largest value among the
 // first 4 chunks per thread, then add every element to its bin.  Returns false
 // (uniformly) when the anchor is not a finite value below 2^20 in magnitude.
-template <bool TDIV, bool PEN>
+template <bool TDIV, bool PEN, bool SC>
 __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X, int V, float& c, uint32_t& km,
                                       uint32_t& nfin, uint32_t& bad) {
   const int tid = threadIdx.x;
@@ -1063,15 +1081,14 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
   float yb[16];
   {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(u * NT + tid);
+    S.chunks(0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int ch = u * NT + tid;
       const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
       float y4[4];
-      X.yt4<TDIV, PEN>(xs, hb, y4);
+      X.yt4<TDIV, PEN, SC>(xs, hb, y4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) yb[4 * u + e] = y4[e];
     }
@@ -1129,15 +1146,14 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
   const int nch = X.nch;
   for (int c0 = 4 * NT; c0 < nch; c0 += 4 * NT) {
     float4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = S.chunk(c0 + u * NT + tid);
+    S.chunks(c0, q);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int ch = c0 + u * NT + tid;
       const uint32_t hb = PEN ? X.nibble(ch) : 0u;
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
       float y4[4];
-      X.yt4<TDIV, PEN>(xs, hb, y4);
+      X.yt4<TDIV, PEN, SC>(xs, hb, y4);
       add4(ch, y4);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1164,8 +1180,19 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
   float c = 0.0f;
   bool anchored;
   const bool tdiv = X.t > 0.0f;
-  if (X.pen) anchored = tdiv ? read1<true, true>(sh, S, X, V, c, km, nfin, bad) : read1<false, true>(sh, S, X, V, c, km, nfin, bad);
-  else anchored = tdiv ? read1<true, false>(sh, S, X, V, c, km, nfin, bad) : read1<false, false>(sh, S, X, V, c, km, nfin, bad);
+  auto r1 = [&](auto tdiv_c, auto pen_c, auto sc_c) -> bool {
+    return read1<decltype(tdiv_c)::value, decltype(pen_c)::value, decltype(sc_c)::value>(sh, S, X, V, c, km, nfin,
+                                                                                         bad);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (X.cap > 0.0f) {
+    if (X.pen) anchored = tdiv ? r1(T_{}, T_{}, T_{}) : r1(F_{}, T_{}, T_{});
+    else anchored = tdiv ? r1(T_{}, F_{}, T_{}) : r1(F_{}, F_{}, T_{});
+  } else {
+    if (X.pen) anchored = tdiv ? r1(T_{}, T_{}, F_{}) : r1(F_{}, T_{}, F_{});
+    else anchored = tdiv ? r1(T_{}, F_{}, F_{}) : r1(F_{}, F_{}, F_{});
+  }
   if (!anchored) return false;
   FL_MARK(1);
   const uint32_t kmx = block_reduce<uint32_t>(km, OpMax(), sh.redu);
@@ -1659,6 +1686,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   X.t = T == 1.0f ? 0.0f : T;  // x / 1 == x exactly: skip the division
   X.rt = X.t > 0.0f ? recip_rt(X.t) : 0.0f;
   X.rpr = recip_rt(RP);
+  X.rcap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
   X.pen = pen;
   X.hbits = hbits_dyn;
   X.nch = nch;
