@@ -271,9 +271,9 @@ __device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f, in
   }
 }
 
-// f(idx, x, hist, valid) for every element: the raw logit and its history bit.
+// f(c, xs, hb) for every chunk c of the row: its raw logits and history bits.
 template <class F>
-__device__ __forceinline__ void row_pass_raw(const Src& S, const Xform& X, F&& f) {
+__device__ __forceinline__ void row_chunks_raw(const Src& S, const Xform& X, F&& f) {
   const int tid = threadIdx.x;
   const int nch = X.nch;
   for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
@@ -282,13 +282,8 @@ __device__ __forceinline__ void row_pass_raw(const Src& S, const Xform& X, F&& f
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = c0 + u * NT + tid;
-      const uint32_t hb = X.nibble(c);
       const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int idx = 4 * c + e;
-        f(idx, xs[e], ((hb >> e) & 1u) != 0u, idx < S.V);
-      }
+      f(c, xs, X.nibble(c));
     }
   }
 }
@@ -1454,24 +1449,49 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
       xl1[i] = i < nr && X.pen ? sh.xlo[1][i] : __builtin_inff();
       xh1[i] = i < nr && X.pen ? sh.xhi[1][i] : -__builtin_inff();
     }
-    auto stage = [&](auto pen_tag) __attribute__((always_inline)) {
-      row_pass_raw(S, X, [&](int idx, float x, bool hist, bool valid) {
-        bool in = false;
+    // (instantiated per range count and history: each element is tested
+    // against the ranges the plan uses, and a chunk takes one ballot)
+    auto stage = [&](auto pen_tag, auto nr_tag) __attribute__((always_inline)) {
+      constexpr bool PEN = decltype(pen_tag)::value;
+      constexpr int NR = decltype(nr_tag)::value;
+      row_chunks_raw(S, X, [&](int c, const float (&xs)[4], uint32_t hb) {
+        bool in[4];
 #pragma unroll
-        for (int i = 0; i < NRANGE; ++i) in |= x >= xl0[i] && x <= xh0[i];
-        if constexpr (decltype(pen_tag)::value) {
-          bool inh = false;
+        for (int e = 0; e < 4; ++e) {
+          const float x = xs[e];
+          bool a = false;
 #pragma unroll
-          for (int i = 0; i < NRANGE; ++i) inh |= x >= xl1[i] && x <= xh1[i];
-          in = hist ? inh : in;
+          for (int i = 0; i < NR; ++i) a |= x >= xl0[i] && x <= xh0[i];
+          if constexpr (PEN) {
+            bool ah = false;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) ah |= x >= xl1[i] && x <= xh1[i];
+            a = ((hb >> e) & 1u) ? ah : a;
+          }
+          in[e] = a && 4 * c + e < V;
         }
-        wave_append(valid && in,
-                    (static_cast<uint64_t>(__float_as_uint(x)) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(idx)),
-                    &sh.ncand, sh.cand);
+        if (__ballot(in[0] || in[1] || in[2] || in[3])) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            wave_append(in[e],
+                        (static_cast<uint64_t>(__float_as_uint(xs[e])) << 32) |
+                            static_cast<uint32_t>(~static_cast<uint32_t>(4 * c + e)),
+                        &sh.ncand, sh.cand);
+        }
       });
     };
-    if (X.pen) stage(std::true_type{});
-    else stage(std::false_type{});
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    auto stage_nr = [&](auto pen_tag) __attribute__((always_inline)) {
+      if (nr <= 1) stage(pen_tag, I1{});
+      else if (nr == 2) stage(pen_tag, I2{});
+      else if (nr == 3) stage(pen_tag, I3{});
+      else stage(pen_tag, I4{});
+    };
+    if (X.pen) stage_nr(std::true_type{});
+    else stage_nr(std::false_type{});
     __syncthreads();
     FL_MARK(5);
     const int ns = static_cast<int>(sh.ncand);
