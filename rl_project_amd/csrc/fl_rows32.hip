@@ -405,25 +405,35 @@ __device__ void bitonic_desc(uint64_t* buf, int n) {
   __syncthreads();
 }
 
-// Descending order of buf[0, n), n <= NT, whose nonzero entries are distinct
-// (zeros sort last): each thread's entry goes to its rank, the number of
+// Descending order of buf[0, n), n <= RANK_SORT_MAX, whose nonzero entries
+// are distinct (zeros sort last): each entry goes to its rank, the number of
 // entries greater than it, counted over broadcast LDS reads -- independent
 // loads, where a bitonic network for a few hundred entries is a chain of
-// dependent LDS round trips.  tmp: scratch of n entries.  Entries of rank
-// >= the nonzero count are left unspecified.
-__device__ void rank_sort_desc(uint64_t* buf, uint64_t* tmp, int n) {
+// dependent LDS round trips.  Every wave counts: the waves holding an entry
+// each take one slice of the others (rank: n counters, tmp: n entries of
+// scratch).  Entries of rank >= the nonzero count are left unspecified.
+__device__ void rank_sort_desc(uint64_t* buf, uint64_t* tmp, uint32_t* rank, int n) {
   const int t = threadIdx.x;
-  const uint64_t mine = t < n ? buf[t] : 0ull;
-  int r = 0;
-  if ((t & ~(WAVE - 1)) < n) {  // waves holding an entry
-    int j = 0;
-    for (; j + 4 <= n; j += 4) {
+  if (t < n) rank[t] = 0;
+  __syncthreads();
+  const int nw = (n + WAVE - 1) / WAVE;  // waves' worth of entries
+  const int w = t / WAVE;
+  if (nw > 0 && w < (NWAVE / nw) * nw) {
+    const int i = (w % nw) * WAVE + (t & (WAVE - 1));
+    const int np = NWAVE / nw, p = w / nw;
+    const int j0 = (n * p) / np, j1 = (n * (p + 1)) / np;
+    const uint64_t mine = i < n ? buf[i] : ~0ull;
+    uint32_t r = 0;
+    int j = j0;
+    for (; j + 4 <= j1; j += 4) {
       const uint64_t a0 = buf[j], a1 = buf[j + 1], a2 = buf[j + 2], a3 = buf[j + 3];
-      r += (a0 > mine ? 1 : 0) + (a1 > mine ? 1 : 0) + (a2 > mine ? 1 : 0) + (a3 > mine ? 1 : 0);
+      r += (a0 > mine ? 1u : 0u) + (a1 > mine ? 1u : 0u) + (a2 > mine ? 1u : 0u) + (a3 > mine ? 1u : 0u);
     }
-    for (; j < n; ++j) r += buf[j] > mine ? 1 : 0;
+    for (; j < j1; ++j) r += buf[j] > mine ? 1u : 0u;
+    if (i < n && r) atomicAdd(&rank[i], r);
   }
-  if (t < n && mine != 0ull) tmp[r] = mine;
+  __syncthreads();
+  if (t < n && buf[t] != 0ull) tmp[rank[t]] = buf[t];
   __syncthreads();
   if (t < n) buf[t] = tmp[t];
   __syncthreads();
@@ -833,39 +843,6 @@ __device__ __forceinline__ void topk_read2(Shared32& sh, const Src& S, const Xfo
   }
 }
 
-// Descending order of buf[0, n), n <= TK_CAND, entries distinct and nonzero:
-// each entry goes to its rank, the number of entries greater than it, counted
-// by every wave -- the waves holding an entry each take one slice of the
-// others (rank: n counters, tmp: n entries of scratch).
-__device__ void topk_sort(uint64_t* buf, uint64_t* tmp, uint32_t* rank, int n) {
-  const int t = threadIdx.x;
-  if (t < n) rank[t] = 0;
-  __syncthreads();
-  const int nw = (n + WAVE - 1) / WAVE;  // waves' worth of entries
-  const int w = t / WAVE;
-  if (nw > 0 && w < (NWAVE / nw) * nw) {
-    const int i = (w % nw) * WAVE + (t & (WAVE - 1));
-    const int np = NWAVE / nw, p = w / nw;
-    const int j0 = (n * p) / np, j1 = (n * (p + 1)) / np;
-    const uint64_t mine = i < n ? buf[i] : ~0ull;
-    uint32_t r = 0;
-    int j = j0;
-    for (; j + 4 <= j1; j += 4) {
-      const uint64_t a0 = buf[j], a1 = buf[j + 1], a2 = buf[j + 2], a3 = buf[j + 3];
-      r += (a0 > mine ? 1u : 0u) + (a1 > mine ? 1u : 0u) + (a2 > mine ? 1u : 0u) + (a3 > mine ? 1u : 0u);
-    }
-    for (; j < j1; ++j) r += buf[j] > mine ? 1u : 0u;
-    if (i < n && r) atomicAdd(&rank[i], r);
-  }
-  __syncthreads();
-  if (t < n) tmp[rank[t]] = buf[t];
-  __syncthreads();
-  if (t < n) buf[t] = tmp[t];
-  __syncthreads();
-}
-
-// The top-k path.  Returns false, with nothing decided, when the row needs
-// another path.  Called by all threads (block-uniform control flow).
 // The bins, zeroed (and the candidate count) before the first barrier of a
 // top-k row.
 __device__ __forceinline__ void topk_init(Shared32& sh) {
@@ -958,7 +935,7 @@ __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xfor
     sh.cand[tid] = (static_cast<uint64_t>(f32_key(y)) << 32) | static_cast<uint32_t>(c);
   }
   FL_MARK(3);
-  topk_sort(sh.cand, sh.cscan, reinterpret_cast<uint32_t*>(sh.cscan + TK_CAND), n);
+  rank_sort_desc(sh.cand, sh.cscan, reinterpret_cast<uint32_t*>(sh.cscan + RANK_SORT_MAX), n);
   FL_MARK(4);
   // The K-th largest y and the largest: a K-th value at -inf, or one that an
   // element below the bin could round to (f of the largest z below the bin
@@ -1513,7 +1490,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     // members first (every member word is nonzero)
     // (the rank sort's work grows as ns^2 / 16 cycles: 1.7 us at 256,
     // 27 us at 1024; the bitonic network's as its steps)
-    if (ns <= RANK_SORT_MAX) rank_sort_desc(sh.cand, sh.cscan, ns);
+    if (ns <= RANK_SORT_MAX) rank_sort_desc(sh.cand, sh.cscan, reinterpret_cast<uint32_t*>(sh.cscan + RANK_SORT_MAX), ns);
     else bitonic_desc(sh.cand, ns);
     FL_MARK(6);
     const int n = ngath;
