@@ -18,7 +18,12 @@ oracle's, except for
                             sums of correctly rounded probabilities, plus
                             every earlier probability whose rounding is open;
                             the group's kept count must lie in the range this
-                            leaves (``_top_p_count_range``);
+                            leaves (``_top_p_count_range``), on the oracle's
+                            survivors or on another survivor set a correct
+                            kernel may reach: open min-p decisions
+                            (``_min_p_survivor_sets``), or on a soft-capped
+                            row the values within 4 units of the K-th value
+                            (``_softcap_top_k_survivor_sets``);
                  selection  the draw must fall within the doubt of the
                             chosen token's cumulative interval
                             (``selection_near``); on a soft-capped row, on the
@@ -149,6 +154,34 @@ def _top_p_count_range(y: np.ndarray, surv: np.ndarray, grp: np.ndarray, top_p: 
     return lo_n, hi_n, float(c_ref[j0] - ps[j0]) if pos.size else 0.0
 
 
+def _softcap_top_k_survivor_sets(y: np.ndarray, top_k: int, cap: int = 16) -> List[np.ndarray]:
+    """Top-k survivor sets (bool [V]) a correct kernel may reach on a
+    soft-capped row: its soft-capped values may lie up to 4 units of the
+    last place from the oracle's (the bound the top-k boundary rule above
+    uses), so the elements within that band of the K-th value may fall on
+    either side of the kernel's own K-th value (``sampling.py:36-38`` keeps
+    every value >= it).  Their masses differ by parts in 10^6, so a top-p cut
+    depends on how many of them survive, not on which: one set per count,
+    from the fewest that still give K survivors to all of them."""
+    V = y.size
+    k = min(int(top_k), V)
+    srt = np.sort(y)[::-1]
+    kth = float(srt[k - 1])
+    band = 4 * np.spacing(np.float32(abs(kth)))
+    core = y > kth + band
+    doubt = np.nonzero(np.abs(y - kth) <= band)[0]
+    doubt = doubt[np.argsort(-y[doubt], kind="stable")]
+    n_core = int(core.sum())
+    sets = []
+    for c in range(max(0, k - n_core), doubt.size + 1):
+        s = core.copy()
+        s[doubt[:c]] = True
+        sets.append(s)
+        if len(sets) >= cap:
+            break
+    return sets
+
+
 def _min_p_survivor_sets(pre_minp: np.ndarray, probs: np.ndarray, min_p: float, dt, cap: int = 8) -> List[np.ndarray]:
     """The min-p survivor sets (bool [V]) that the rounding doubt leaves open
     (``sampling.py:40-43``): the oracle's first, then the others.
@@ -267,6 +300,11 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                         minp_sets = _min_p_survivor_sets(pm, F.softmax(pre_minp, dim=-1)[0].double().numpy(),
                                                          p.min_p, dt)[1:]
                     sets = sets + minp_sets
+                n_minp = len(sets)
+                if softcap > 0 and p.top_k and 0 < p.top_k < V and not (p.min_p and p.min_p > 0):
+                    # (a top-p cut runs over the top-k survivors the kernel's
+                    # own soft-capped values leave)
+                    sets = sets + _softcap_top_k_survivor_sets(y, p.top_k)
                 for k, s in enumerate(sets):
                     lo_n, hi_n, excl = _top_p_count_range(y, s, grp, p.top_p, dt)
                     if lo_n <= ng <= hi_n:
@@ -274,7 +312,9 @@ def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tens
                         margins.append(abs(excl - p.top_p) / max(p.top_p, 1e-30))
                         verdict.details.append(f"near top-p y={v:.9g} excl={excl:.9g} top_p={p.top_p} "
                                                f"kept {ng} in [{lo_n}, {hi_n}]" +
-                                               (f" (min-p survivors: open set {k})" if k else ""))
+                                               (f" (min-p survivors: open set {k})" if 0 < k < n_minp else "") +
+                                               (f" (soft-cap top-k survivors: set {k - n_minp})" if k >= n_minp
+                                                else ""))
                         break
             if not explained:
                 verdict.kind = "MISMATCH"

@@ -425,3 +425,43 @@ def test_top_p_cut_on_the_kernels_open_min_p_survivors_f16():
         gk[grp[:n]] = True
         v = _kind(x, p, float(w.uniforms[b]), keep, r.token, gk, None, softcap=w.softcap)
         assert v.kind == kind, (n, v.kind, v.details[-2:])
+
+
+def test_top_p_cut_on_the_kernels_soft_capped_top_k_survivors_f32():
+    """A float32 row of the sampling sweep (seed 202175, row 2: V=151936,
+    soft-cap 5 over logits near 25, T 1, top-k 1000, top-p 0.9, penalty 1.2):
+    the soft-cap packs the largest values into a few units of the last place
+    below 5.0, and three elements tie at the K-th value.  On the GPU the
+    kernel's soft-cap puts one of them (index 74521) one unit lower, so its
+    top-k keeps 1001 values where the oracle keeps 1002; the top-p cut over
+    that mass keeps 901 against 902.  The classifier judges the cut on the
+    top-k survivor sets that soft-capped values within 4 units of the K-th
+    value may leave (1000 to 1003 survivors here, cuts at 900 to 903): 901 is
+    NEAR, cuts at 899 and 906 stay MISMATCH."""
+    from tests.helpers import row_params, sweep_case
+
+    w, _ = sweep_case(202175)
+    b = 2
+    x = w.logits[b]
+    p = row_params(w, b)
+    assert x.dtype == torch.float32 and x.numel() == 151936 and w.softcap == 5.0
+    assert (p.top_k, p.min_p) == (1000, 0.0) and abs(p.top_p - 0.9) < 1e-7
+    u = float(w.uniforms[b])
+    r, keep, y = _oracle(x, p, u, softcap=w.softcap)
+    assert int(keep.sum()) == 902
+    kth = float(torch.sort(y, descending=True).values[p.top_k - 1])
+    assert torch.nonzero(y == kth).flatten().tolist() == [24838, 74521, 134780]
+    # the kernel's values: the oracle's, with index 74521 one unit lower
+    yk = y.clone()
+    yk[74521] = float(np.nextafter(np.float32(kth), np.float32(-np.inf)))
+    gk = torch.isfinite(O._top_p(O._top_k(yk[None].clone(), p.top_k), p.top_p, True)[0])
+    assert int(gk.sum()) == 901
+    v = _kind(x, p, u, keep, r.token, gk, None, softcap=w.softcap)
+    assert v.kind == "NEAR", v.details[-2:]
+    # cuts outside every survivor set's range
+    order = torch.sort(y, descending=True, stable=True).indices
+    for n in (899, 906):
+        bad = torch.zeros_like(keep)
+        bad[order[:n]] = True
+        v = _kind(x, p, u, keep, r.token, bad, None, softcap=w.softcap)
+        assert v.kind == "MISMATCH", (n, v.details[-2:])

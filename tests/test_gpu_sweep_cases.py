@@ -27,3 +27,25 @@ def test_sweep_seed_71183_f16_top_p_after_an_open_min_p_boundary():
     grp = torch.nonzero(y == 7.04296875).flatten()
     assert grp.numel() == 535
     assert int(keep[ok_rows.index(b)][grp].sum()) == 276
+
+
+def test_sweep_seed_202175_f32_top_p_over_soft_capped_top_k_survivors():
+    """float32, V=151936, soft-cap 5 over logits near 25 (8 rows).  Row 2
+    (top-k 1000, top-p 0.9): three elements tie at the K-th value in the
+    oracle, and the kernel's soft-cap puts one of them (index 74521) a unit
+    lower, so its top-k keeps 1001 and its top-p cut 901 where the oracle
+    keeps 1002 and 902.  Every row must classify without MISMATCH, and row 2
+    must keep exactly the oracle's 901 largest values."""
+    w, ok_rows, st, summ, verdicts, toks, keep = run_sweep_case(202175)
+    print(f"seed 202175: status {st.tolist()} {summ}", flush=True)
+    assert summ["MISMATCH"] == 0, [v.details[:3] for v in verdicts if not v.ok]
+    assert 2 in ok_rows
+    from oracle import sampler_oracle as O
+    from tests.helpers import row_params
+
+    p = row_params(w, 2)
+    y = O.pre_filter_values(w.logits[2][None], p.temperature, p.repetition_penalty, p.history, w.softcap)[0]
+    order = torch.sort(y, descending=True, stable=True).indices
+    want = torch.zeros_like(keep[0])
+    want[order[:901]] = True
+    assert torch.equal(keep[ok_rows.index(2)], want)
