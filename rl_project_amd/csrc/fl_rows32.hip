@@ -574,9 +574,10 @@ struct RowOut {
 };
 
 // ------------------------------------------------------------ top-k path
-// Rows with top-k on (a request's default keeps 50, inference/requests.py:26):
-// every decision of sampling.py:36-61 acts on the top-k survivors, which a
-// histogram finds without the filtered values of the whole row.  The value
+// Rows with top-k on, up to TK_MAX (a request's default keeps 50,
+// inference/requests.py:26): every decision of sampling.py:36-61 acts on
+// the top-k survivors, which a histogram finds without the filtered values of
+// the whole row.  The value
 // y = RN(z / t) + 0 (sampling.py:33-34) is a non-decreasing function f of the
 // penalised value z (sampling.py:30), so the K-th largest y is f of the K-th
 // largest z, and only candidates need y:
@@ -596,8 +597,8 @@ struct RowOut {
 //            64 at a time: min-p, top-p and the inverse CDF on exact 2^-45
 //            masses fx45(exp(y - M)) -- the multi-pass path's arithmetic,
 //            element by element.
-constexpr int TK_MAX = 1024;            // top-k values this path serves
 constexpr int TK_CAND = RANK_SORT_MAX;  // candidates it sorts and decides
+constexpr int TK_MAX = TK_CAND;         // top-k values it serves (a row has at least K candidates)
 constexpr int TK_TILE = 8;              // chunks per thread whose keys read 1 keeps in registers
 constexpr int TK_SH = 19;               // bin of a key: key >> TK_SH
 constexpr int TK_NB = 1 << (32 - TK_SH);
