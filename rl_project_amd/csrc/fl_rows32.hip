@@ -878,7 +878,7 @@ __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xfor
     if (sc) topk_hist_move<true>(sh, S, X, V, h, bad);
     else topk_hist_move<false>(sh, S, X, V, h, bad);
   }
-  if (block_reduce<uint32_t>(bad ? 1u : 0u, OpMax(), sh.redu) != 0u) return false;
+  __syncthreads();  // (every add and move before the scan reads the bins)
   FL_MARK(11);
 
   // ---------------------------------------------- bin of the K-th largest value
@@ -898,10 +898,14 @@ __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xfor
     uint32_t sum = 0;
 #pragma unroll
     for (int q = 0; q < TK_BPT; ++q) sum += c[q];
+    // (the scan also counts the threads that saw a NaN, in bits 20 and up:
+    // a row holds at most 2^18 values and a block 1024 threads)
     uint32_t tot;
-    const uint32_t ex = block_excl_scan<uint32_t>(sum, sh.redu, &tot);
+    const uint32_t ex = block_excl_scan<uint32_t>(sum | (bad ? 1u << 20 : 0u), sh.redu, &tot) & 0xFFFFFu;
+    // (with a NaN no bin is picked: pick_bin stays -1 and the two-read path
+    // reports the row)
     const uint32_t k = static_cast<uint32_t>(K);
-    if (ex < k && ex + sum >= k) {
+    if ((tot >> 20) == 0u && ex < k && ex + sum >= k) {
       uint32_t run = ex;
       bool done = false;
 #pragma unroll
