@@ -16,22 +16,18 @@
 #include "../../include/fl_sampler.h"
 
 // Phase timestamps for kernel tuning builds (-DFL_PHASE_TIMES): thread 0 of
-// work-groups 0..3 records the constant-rate wall clock at each FL_MARK (and
-// every work-group its first and last mark).
+// each of the first 1024 work-groups records the constant-rate wall clock at
+// each FL_MARK(n), n < 16, in slot 16 * blockIdx.x + n.
 #ifdef FL_PHASE_TIMES
-// [0, 192): marks of blocks 0..3; [192, 192 + 2*1024): start / end of every block
-static __device__ uint64_t fl_phase_ts[4 * 16 * 2 + 64 + 2 * 1024];
+#define FL_PHASE_SLOTS (16 * 1024)
+static __device__ uint64_t fl_phase_ts[FL_PHASE_SLOTS];
 #ifndef FL_MARK_MASK
 #define FL_MARK_MASK 0xFFFF  // marks recorded (bit n: FL_MARK(n)); fewer marks, fewer spills
 #endif
 #define FL_MARK(n)                                                              \
   do {                                                                          \
-    if (((FL_MARK_MASK >> (n)) & 1) && threadIdx.x == 0) {                      \
-      const uint64_t t_ = wall_clock64();                                       \
-      if (blockIdx.x < 4) fl_phase_ts[blockIdx.x * 16 + (n)] = t_;              \
-      if (((n) == 0 || (n) == 9) && blockIdx.x < 1024)                          \
-        fl_phase_ts[192 + 2 * blockIdx.x + ((n) == 9)] = t_;                    \
-    }                                                                           \
+    if (((FL_MARK_MASK >> (n)) & 1) && threadIdx.x == 0 && blockIdx.x < 1024)   \
+      fl_phase_ts[blockIdx.x * 16 + (n)] = wall_clock64();                      \
   } while (0)
 #else
 #define FL_MARK(n) \

@@ -43,6 +43,11 @@ constexpr int NSTEP = 512;                        // compaction steps of 128 ord
 constexpr int SPW = NSTEP / NWAVE;                // steps per wave
 constexpr int HPRE = 2;                          // history ids per thread loaded ahead of the row
 constexpr int EARLY_CHUNKS = 2;                  // row chunks per thread requested before the LDS clear
+#ifndef FL_LOOKAHEAD
+#define FL_LOOKAHEAD 4
+#endif
+constexpr int LOOKAHEAD = FL_LOOKAHEAD;          // row chunks per thread in flight while counting
+static_assert(LOOKAHEAD >= EARLY_CHUNKS && LOOKAHEAD <= NCH, "lookahead window");
 constexpr int MAX_HEAVY = 8;                     // patterns with more than 65535 values (at most 5 exist)
 
 static_assert(NSLOT * NT * 8 == FL_MAX_VOCAB_16 && NSLOT >= NCH, "identification slots cover the longest row");
@@ -393,19 +398,6 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
   lds_barrier();
   FL_MARK(1);
 
-  // ------------------------------------------------ row loads (VGPR tile)
-  // (unconditional: behind a branch, the compiler's wait for the history ids
-  // would also wait for the row on the path that loaded it; a row the fast
-  // path does not take gets an empty range, so its loads return zeros)
-  // (issued in chunk order, pinned by scheduling barriers: the count pass
-  // takes the chunks in that order, and counting a chunk whose load was issued
-  // late would hold back the counting of all chunks after it)
-#pragma unroll
-  for (int j = EARLY_CHUNKS; j < NCH; ++j) {
-    d[j] = buf_load16_once(rrow, 16u * tid, 16u * NT * j);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
   // u outside [0, 1) (or NaN) is clamped into it
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const float CAP = a.softcap;
@@ -453,6 +445,22 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
 #pragma unroll
   for (int k = 0; k < HPRE; ++k) xh[k] = row[own[k] ? hpre[k] : 0];
 
+  // ------------------------------------------------ row loads (VGPR tile)
+  // Issued after the history gathers: a wave's loads complete in issue order,
+  // so the gathered logits arrive ahead of the row's chunks and the penalty
+  // moves are made before the counting (moves and counts commute).
+  // (unconditional: behind a branch, the compiler's wait for the history ids
+  // would also wait for the row on the path that loaded it; a row the fast
+  // path does not take gets an empty range, so its loads return zeros)
+  // (issued in chunk order, pinned by scheduling barriers: the count pass
+  // takes the chunks in that order, and counting a chunk whose load was issued
+  // late would hold back the counting of all chunks after it)
+#pragma unroll
+  for (int j = EARLY_CHUNKS; j < LOOKAHEAD; ++j) {
+    d[j] = buf_load16_once(rrow, 16u * tid, 16u * NT * j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
   // ------------------------------------------------ count patterns
   // Raw -inf values (a masked vocabulary) stay out of the pattern counts,
   // where more than 65535 of them would wrap a 16-bit counter, and go to a
@@ -472,29 +480,37 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       atomicAdd(&sh.hist[raw == NEG_INF_RAW ? inf_word : raw >> 1], 1u + (raw & 1u) * 0xFFFFu);
     }
   };
-  if constexpr (!HEAVY) {  // (the recounting body counts in heavy_recount)
-  if (fast_row) {
+  // The count of the two patterns of a word w (no -inf or negative NaN among
+  // them): pattern p's counter is half p & 1 of word p >> 1, so the byte
+  // address is (p << 1) & 0x1FFFC and the increment 1 + (p & 1) * 0xFFFF.
+  // Written as instructions (4 VALU per value; the compiler's compare-and-
+  // select form takes 7 with the -inf test).
+  const uint32_t ffff = 0xFFFFu;
+  auto count_pair = [&](uint32_t w) {
+    uint32_t a0, a1, i0, i1;
+    asm volatile(
+        "v_lshlrev_b32 %0, 1, %4\n\t"
+        "v_and_b32 %0, 0x1fffc, %0\n\t"
+        "v_lshrrev_b32 %1, 15, %4\n\t"
+        "v_and_b32 %1, 0x1fffc, %1\n\t"
+        "v_and_b32 %2, 1, %4\n\t"
+        "v_mad_u32_u24 %2, %2, %5, 1\n\t"
+        "v_bfe_u32 %3, %4, 16, 1\n\t"
+        "v_mad_u32_u24 %3, %3, %5, 1"
+        : "=&v"(a0), "=&v"(a1), "=&v"(i0), "=&v"(i1)
+        : "v"(w), "s"(ffff));
+    atomicAdd(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sh.hist) + a0), i0);
+    atomicAdd(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sh.hist) + a1), i1);
+  };
+  // a chunk holding -inf or a negative NaN (raw patterns >= the -inf
+  // pattern) takes the per-value count: one packed maximum per word
+  auto chunk_has_top_patterns = [&](const uint32_t (&w4)[4]) -> bool {
+    u16x2 m = __builtin_bit_cast(u16x2, w4[0]);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j * NT + tid < nfull) {
-        const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) count((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
-      }
-    }
-  } else {
-    for (int c = tid; c < nfull; c += NT) {
-      const uint4 q = load_chunk16(row, c, V, ALIGNED);
-      const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) count((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
-    }
-  }
-  if (tid == 0)
-    for (int i = nfull * 8; i < V; ++i) count(row[i]);
-  }
-
-  FL_MARK(12);
+    for (int k = 1; k < 4; ++k) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w4[k]));
+    return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y)) >= NEG_INF_RAW;
+  };
+  static_assert(HIST_WORDS * 4 == 0x20000, "pattern byte addresses are 17 bits");
   // ------------------------------------------------ repetition penalty
   // each unique id moves one count from its pattern to its penalised pattern
   auto move = [&](uint32_t raw, uint32_t z, uint32_t zp) {
@@ -510,7 +526,10 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
     move(raw, z, penalised_bits<D>(z, RP));
   };
   // the patterns of the owned prefetched ids, kept for the identification
-  // (16 bits each, in one VGPR)
+  // (16 bits each, in one VGPR); their moves are made before the counting
+  // (the packed counters add modulo 2^32, so a count taken below zero for a
+  // while borrows from its neighbour and repays it: the order of the adds
+  // does not matter)
   static_assert(HPRE == 2, "two patterns per word");
   uint32_t hz = 0;
 #pragma unroll
@@ -521,6 +540,45 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
       move(xh[k], z, penalised_bits<D>(z, RP));
     }
   }
+  if constexpr (!HEAVY) {  // (the recounting body counts in heavy_recount)
+  if (fast_row) {
+    // Software-pipelined: chunk j + LOOKAHEAD is requested as chunk j is
+    // counted, so each wave keeps a few chunks in flight and every wave's
+    // data arrives spread over the whole stream.  (Requested all at once, the
+    // oldest waves' loads are served first and the youngest waves receive
+    // their whole tile, and count it, only at the end of the stream.)
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j + LOOKAHEAD < NCH) d[j + LOOKAHEAD] = buf_load16_once(rrow, 16u * tid, 16u * NT * (j + LOOKAHEAD));
+      __builtin_amdgcn_sched_barrier(0);
+      if (j * NT + tid < nfull) {
+        const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
+        if (SC || chunk_has_top_patterns(w4)) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) count((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) count_pair(w4[k]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int j = LOOKAHEAD; j < NCH; ++j) d[j] = make_uint4(0, 0, 0, 0);
+    for (int c = tid; c < nfull; c += NT) {
+      const uint4 q = load_chunk16(row, c, V, ALIGNED);
+      const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) count((w4[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu);
+    }
+  }
+  if (tid == 0)
+    for (int i = nfull * 8; i < V; ++i) count(row[i]);
+  }
+
+  FL_MARK(12);
+  // ids past the prefetched ones (and every id of a row past the tile)
   if (!wide) {
     for (int i = tid + ((hist_rows && !HEAVY) ? HPRE * NT : 0); i < H; i += NT) {
       const int id = hid[i];
@@ -1343,6 +1401,7 @@ __device__ __forceinline__ bool row_body(const fl_sample_args a, const int ALIGN
 template <class D, bool SC>
 __global__ __launch_bounds__(NT) void k_sample_rows16(const fl_sample_args a, const int ALIGNED, const int SC_ELEM_IN) {
   __shared__ Shared16 sh;
+  FL_MARK(11);  // (kernel entry)
   row_body<D, SC, false>(a, ALIGNED, SC_ELEM_IN, sh);
 }
 
@@ -1386,7 +1445,7 @@ hipError_t launch_sample_rows16(const fl_sample_args& a, hipStream_t s) {
 #ifdef FL_PHASE_TIMES
 // Tuning builds only: copy the phase timestamps recorded by the last launch.
 extern "C" int fl_debug_phase_ts(uint64_t* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * (192 + 2048), 0,
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * FL_PHASE_SLOTS, 0,
                              hipMemcpyDeviceToHost) ==
                  hipSuccess ? 0 : -1;
 }

@@ -2187,7 +2187,7 @@ hipError_t launch_sample_rows32(const fl_sample_args& a, hipStream_t s) {
 #ifdef FL_PHASE_TIMES
 // Tuning builds only: copy the phase timestamps this kernel recorded.
 extern "C" int fl_debug_phase_ts32(uint64_t* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * (192 + 2048), 0,
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(fl_phase_ts), sizeof(uint64_t) * FL_PHASE_SLOTS, 0,
                              hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 #endif
