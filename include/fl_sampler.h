@@ -209,7 +209,7 @@ typedef struct fl_spec_args {
   int32_t* out_n_accepted;         /* [batch] */
   int64_t* out_tokens;             /* [batch, k+1] */
   float* out_ratio;                /* [batch, k] or NULL */
-  void* workspace;                 /* NULL, or fl_spec_workspace_bytes(batch) bytes of device memory */
+  void* workspace;                 /* NULL, or at least fl_spec_workspace_bytes(batch) bytes of device memory */
   int64_t workspace_bytes;
 } fl_spec_args;
 
@@ -225,6 +225,15 @@ int fl_spec_verify(const fl_spec_args* args, void* stream);
 /* Bytes of workspace fl_spec_verify uses for `batch` sequences (no counterpart
  * in the reference, which verifies one sequence at a time). */
 int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes);
+
+/* Bytes of a workspace with which fl_spec_verify also caches each rejected
+ * sequence's residual max(0, p - q) (4 bytes per vocabulary entry and
+ * sequence): the second slice pass and the draw then read it instead of
+ * recomputing both rows' filtered probabilities.  Results are identical.
+ * A workspace of at least this size (16-byte aligned) takes the cached path;
+ * one of at least fl_spec_workspace_bytes the uncached one.  No counterpart
+ * in the reference. */
+int fl_spec_cache_workspace_bytes(int64_t batch, int64_t vocab, size_t* out_bytes);
 
 /*
  * fl_spec_verify on its sliced path with no workspace argument and no

@@ -131,6 +131,8 @@ def lib() -> ctypes.CDLL:
     handle.fl_spec_verify_static.restype = ctypes.c_int
     handle.fl_spec_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
     handle.fl_spec_workspace_bytes.restype = ctypes.c_int
+    handle.fl_spec_cache_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
+    handle.fl_spec_cache_workspace_bytes.restype = ctypes.c_int
     handle.fl_lm_head_sample.argtypes = [ctypes.POINTER(LmHeadArgs), _p]
     handle.fl_lm_head_sample.restype = ctypes.c_int
     handle.fl_lm_head_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_size_t)]
@@ -167,5 +169,5 @@ def stream_handle(device: torch.device) -> int:
 
 
 EXPORTED_SYMBOLS = ("fl_sample", "fl_apply_filter", "fl_spec_verify", "fl_spec_verify_static",
-                    "fl_spec_workspace_bytes", "fl_lm_head_sample", "fl_lm_head_workspace_bytes", "fl_row_stats",
+                    "fl_spec_workspace_bytes", "fl_spec_cache_workspace_bytes", "fl_lm_head_sample", "fl_lm_head_workspace_bytes", "fl_row_stats",
                     "fl_last_error", "fl_abi_version")

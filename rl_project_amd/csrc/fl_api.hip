@@ -223,4 +223,13 @@ int fl_spec_workspace_bytes(int64_t batch, size_t* out_bytes) {
   return ok();
 }
 
+int fl_spec_cache_workspace_bytes(int64_t batch, int64_t vocab, size_t* out_bytes) {
+  if (out_bytes == nullptr) return fail(FL_EINVAL, "fl_spec_cache_workspace_bytes: out_bytes is NULL");
+  if (batch < 0 || batch > 0x7fffffff || vocab < 1 || vocab > FL_MAX_VOCAB_F32)
+    return fail(FL_EINVAL, "fl_spec_cache_workspace_bytes: bad batch %lld or vocab %lld", static_cast<long long>(batch),
+                static_cast<long long>(vocab));
+  *out_bytes = fl::spec_cache_workspace_bytes(batch, vocab);
+  return ok();
+}
+
 }  // extern "C"

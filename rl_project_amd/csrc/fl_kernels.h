@@ -17,8 +17,9 @@ hipError_t launch_apply_filter(const fl_sample_args& a, const fl_row_desc* desc,
 
 // Speculative accept / residual resample, one work-group per sequence.
 hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s);
-hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, hipStream_t s);
+hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, size_t workspace_bytes, hipStream_t s);
 size_t spec_workspace_bytes(int64_t batch);
+size_t spec_cache_workspace_bytes(int64_t batch, int64_t vocab);
 // The same with the library's static device scratch (no allocation).
 hipError_t launch_spec_verify_static(const fl_spec_args& a, hipStream_t s);
 size_t spec_static_scratch_bytes();

@@ -252,22 +252,127 @@ __device__ __forceinline__ uint64_t range_sum(const PairRows<D>& R, int c0, int 
   return acc;
 }
 
+// The residual cache: one row of max(0, p - q) per sequence (the rejected
+// position's), written by the first slice pass so that the second pass and
+// the pick read 4 bytes per element instead of recomputing both rows'
+// filtered probabilities.  Row stride: the vocabulary rounded up to 8 floats,
+// so that every chunk of a row (4 or 8 elements, 16-byte aligned) lies inside
+// its row's buffer range whole; the padding holds zeros.
+__host__ __device__ inline int64_t spec_cache_ld(int64_t vocab) { return (vocab + 7) & ~int64_t(7); }
+
+template <class D>
+struct CachedRow {
+  static constexpr int N = Chunk<D>::N;  // elements per chunk, as in PairRows
+  __amdgpu_buffer_rsrc_t rr;
+  int V;
+  __device__ CachedRow(float* cache, int64_t ld, int64_t b, int V_) : V(V_) {
+    rr = row_rsrc(cache + b * ld, static_cast<uint32_t>(ld) * 4u);
+  }
+  // the cached residuals of chunk c (zeros past the row)
+  __device__ __forceinline__ void load(int c, float (&r)[N]) const {
+#pragma unroll
+    for (int h = 0; h < N / 4; ++h) {
+      const uint4 u = buf_load16(rr, 16u * static_cast<uint32_t>(N / 4 * c + h), 0u);
+      r[4 * h] = __uint_as_float(u.x);
+      r[4 * h + 1] = __uint_as_float(u.y);
+      r[4 * h + 2] = __uint_as_float(u.z);
+      r[4 * h + 3] = __uint_as_float(u.w);
+    }
+  }
+  __device__ __forceinline__ void store(int c, const float (&r)[N]) const {
+#pragma unroll
+    for (int h = 0; h < N / 4; ++h) {
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int,
+                             make_uint4(__float_as_uint(r[4 * h]), __float_as_uint(r[4 * h + 1]),
+                                        __float_as_uint(r[4 * h + 2]), __float_as_uint(r[4 * h + 3]))),
+          rr, static_cast<int>(16u * static_cast<uint32_t>(N / 4 * c + h)), 0, 0);
+    }
+  }
+  // g(e, i, w) with w = rn(r / den), the weight of Weight<D> for r > 0 sums
+  template <class G>
+  __device__ __forceinline__ void weights(int c, float den, G&& g) const {
+    float r[N];
+    load(c, r);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const int i = N * c + e;
+      if (i < V) g(e, i, D::rn(r[e] / den));
+    }
+  }
+};
+
+// range_sum of the residual that also stores it in the cache
+template <class D>
+__device__ __forceinline__ uint64_t range_sum_store(const PairRows<D>& R, const CachedRow<D>& C, int c0, int c1,
+                                                    int nthreads) {
+  constexpr int U = 4, N = PairRows<D>::N;
+  uint64_t acc = 0;
+  for (int cb = c0 + static_cast<int>(threadIdx.x); cb < c1; cb += U * nthreads) {
+    float xt[U][N], xd[U][N];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+      if (c < c1) R.load(c, xt[u], xd[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+      if (c < c1) {
+        float r[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) r[e] = 0.0f;
+        R.eval(c, xt[u], xd[u], [&](int e, int, float p, float q) {
+          r[e] = resid_of<D>(p, q);
+          acc += fx45(r[e]);
+        });
+        C.store(c, r);
+      }
+    }
+  }
+  return acc;
+}
+
+// range_sum of the weights read from the cache
+template <class D>
+__device__ __forceinline__ uint64_t range_sum_cached(const CachedRow<D>& C, float den, int c0, int c1, int nthreads) {
+  constexpr int U = 4, N = CachedRow<D>::N;
+  uint64_t acc = 0;
+  for (int cb = c0 + static_cast<int>(threadIdx.x); cb < c1; cb += U * nthreads) {
+    float r[U][N];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+      if (c < c1) C.load(c, r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * nthreads;
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        if (c < c1 && N * c + e < C.V) acc += fx45(D::rn(r[u][e] / den));
+    }
+  }
+  return acc;
+}
+
 // Inverse CDF over chunks [c0, c1) with NT threads: the first index whose
 // inclusive weight, added to `base`, exceeds `target`.  With `own_target`
 // the target is floor(u * total) of the range itself and base is 0.  Records
 // each (round, wave) segment's weight sum, then wave 0 finds the segment and
 // scans its 64 chunks.  Returns the index or -1 (to every thread).
-template <class D>
-__device__ int pick_in_range(SharedSpec& sh, const PairRows<D>& R, const Weight<D>& wt, int c0, int c1, bool own_target,
-                             float u, uint64_t base, uint64_t target) {
-  constexpr int N = PairRows<D>::N;
+// (wchunk(c, g) calls g(e, i, w) with the weight w of each element i = N c + e
+// of chunk c below the row's length)
+template <int N, class WChunk>
+__device__ int pick_in_range(SharedSpec& sh, WChunk&& wchunk, int c0, int c1, bool own_target, float u, uint64_t base,
+                             uint64_t target) {
   const int tid = threadIdx.x;
   const int w = tid / WAVE, lane = tid & (WAVE - 1);
   const int nround = (c1 - c0 + NT - 1) / NT;
   for (int k = 0; k < nround; ++k) {
     const int c = c0 + k * NT + tid;
     uint64_t lw = 0;
-    if (c < c1) R.chunk(c, [&](int, int, float p, float q) { lw += fx45(wt(p, q)); });
+    if (c < c1) wchunk(c, [&](int, int, float w) { lw += fx45(w); });
     lw = wave_reduce(lw, OpAdd());
     if (lane == 0) sh.seg[k * NWAVE + w] = lw;
   }
@@ -304,8 +409,8 @@ __device__ int pick_in_range(SharedSpec& sh, const PairRows<D>& R, const Weight<
 #pragma unroll
       for (int e = 0; e < N; ++e) wl[e] = 0;
       if (c < c1) {
-        R.chunk(c, [&](int e, int, float p, float q) {
-          wl[e] = fx45(wt(p, q));
+        wchunk(c, [&](int e, int, float w) {
+          wl[e] = fx45(w);
           lc += wl[e];
         });
       }
@@ -345,23 +450,35 @@ __host__ __device__ inline int spec_slices(int64_t batch) {
 
 // Workspace of the sliced path: int32 state[batch] (rejected position or -1),
 // padded to 8 bytes, then uint64 part1[batch * S] and part2[batch * S].
+// A workspace of at least spec_cache_bytes(batch, vocab) bytes also holds
+// the residual cache (float[batch][spec_cache_ld(vocab)], 16-byte aligned).
 struct SpecWs {
   int32_t* state;
   uint64_t* part1;
   uint64_t* part2;
+  float* cache;  // or nullptr
+  int64_t cache_ld;
   int S;
 };
 __host__ __device__ inline size_t spec_ws_bytes(int64_t batch) {
   const int S = spec_slices(batch);
   return ((static_cast<size_t>(batch) * 4 + 7) & ~static_cast<size_t>(7)) + 16u * static_cast<size_t>(batch) * S;
 }
-__host__ __device__ inline SpecWs spec_ws(void* p, int64_t batch) {
+__host__ __device__ inline size_t spec_cache_bytes(int64_t batch, int64_t vocab) {
+  return ((spec_ws_bytes(batch) + 15) & ~static_cast<size_t>(15)) +
+         4u * static_cast<size_t>(batch) * static_cast<size_t>(spec_cache_ld(vocab));
+}
+__host__ __device__ inline SpecWs spec_ws(void* p, int64_t batch, size_t bytes, int64_t vocab) {
   SpecWs w;
   w.S = spec_slices(batch);
   w.state = static_cast<int32_t*>(p);
   char* q = static_cast<char*>(p) + ((static_cast<size_t>(batch) * 4 + 7) & ~static_cast<size_t>(7));
   w.part1 = reinterpret_cast<uint64_t*>(q);
   w.part2 = w.part1 + batch * w.S;
+  const bool cached = bytes >= spec_cache_bytes(batch, vocab) && (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+  w.cache = cached ? reinterpret_cast<float*>(static_cast<char*>(p) + ((spec_ws_bytes(batch) + 15) & ~static_cast<size_t>(15)))
+                   : nullptr;
+  w.cache_ld = spec_cache_ld(vocab);
   return w;
 }
 
@@ -393,7 +510,8 @@ __global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
     const uint64_t rsum = block_reduce<uint64_t>(lr, OpAdd(), sh.redq);
     const Weight<D> wt(rsum);
     const float U = fminf(fmaxf(a.u_resample[b], 0.0f), 0.99999994f);
-    const int t = pick_in_range(sh, R, wt, 0, R.nch, true, U, 0, 0);
+    auto wchunk = [&](int c, auto&& g) { R.chunk(c, [&](int e, int i, float p, float q) { g(e, i, wt(p, q)); }); };
+    const int t = pick_in_range<PairRows<D>::N>(sh, wchunk, 0, R.nch, true, U, 0, 0);
     tok = t < 0 ? R.V - 1 : t;
   }
   if (tid == 0) write_tail(a, b, n_acc, tok);
@@ -426,13 +544,20 @@ __global__ __launch_bounds__(NT_PART) void k_spec_part(const fl_spec_args a, Spe
   const int c0 = min(R.nch, s * cps), c1 = min(R.nch, c0 + cps);
   uint64_t v;
   if constexpr (!PASS2) {
-    v = range_sum(R, c0, c1, NT_PART, [](float p, float q) { return resid_of<D>(p, q); });
+    if (ws.cache != nullptr)
+      v = range_sum_store(R, CachedRow<D>(ws.cache, ws.cache_ld, b, R.V), c0, c1, NT_PART);
+    else
+      v = range_sum(R, c0, c1, NT_PART, [](float p, float q) { return resid_of<D>(p, q); });
   } else {
     // sum(r) over the slices: one slice per lane, in every wave
     const int lane = threadIdx.x & (WAVE - 1);
     const uint64_t rsum = wave_reduce(lane < ws.S ? ws.part1[b * ws.S + lane] : 0ull, OpAdd());
     const Weight<D> wt(rsum);
-    v = range_sum(R, c0, c1, NT_PART, wt);
+    // (all-zero residuals draw from p: the rows are read again)
+    if (ws.cache != nullptr && !wt.use_p)
+      v = range_sum_cached(CachedRow<D>(ws.cache, ws.cache_ld, b, R.V), wt.den, c0, c1, NT_PART);
+    else
+      v = range_sum(R, c0, c1, NT_PART, wt);
   }
   v = block_reduce<uint64_t, OpAdd, NT_PART / WAVE>(v, OpAdd(), red);
   if (threadIdx.x == 0) (PASS2 ? ws.part2 : ws.part1)[b * ws.S + s] = v;
@@ -462,11 +587,20 @@ __global__ __launch_bounds__(NT) void k_spec_pick(const fl_spec_args a, SpecWs w
   const uint64_t base = readlane64(inc - p2, s);
   const int cps = (R.nch + ws.S - 1) / ws.S;
   const int c0 = min(R.nch, s * cps), c1 = min(R.nch, c0 + cps);
-  const int t = pick_in_range(sh, R, wt, c0, c1, false, U, base, target);
+  int t;
+  if (ws.cache != nullptr && !wt.use_p) {
+    const CachedRow<D> C(ws.cache, ws.cache_ld, b, R.V);
+    auto wchunk = [&](int c, auto&& g) { C.weights(c, wt.den, g); };
+    t = pick_in_range<PairRows<D>::N>(sh, wchunk, c0, c1, false, U, base, target);
+  } else {
+    auto wchunk = [&](int c, auto&& g) { R.chunk(c, [&](int e, int i, float p, float q) { g(e, i, wt(p, q)); }); };
+    t = pick_in_range<PairRows<D>::N>(sh, wchunk, c0, c1, false, U, base, target);
+  }
   if (threadIdx.x == 0) write_tail(a, b, pos, t < 0 ? R.V - 1 : t);
 }
 
 size_t spec_workspace_bytes(int64_t batch) { return spec_ws_bytes(batch); }
+size_t spec_cache_workspace_bytes(int64_t batch, int64_t vocab) { return spec_cache_bytes(batch, vocab); }
 
 // ---------------------------------------------------------------- scratch that needs no allocation
 // The sliced path's workspace for up to FL_SPEC_STATIC_MAX_BATCH sequences
@@ -506,19 +640,21 @@ hipError_t spec_static_scratch(void** out) {
   return hipSuccess;
 }
 
-hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s) { return launch_spec_verify_on(a, a.workspace, s); }
+hipError_t launch_spec_verify(const fl_spec_args& a, hipStream_t s) {
+  return launch_spec_verify_on(a, a.workspace, static_cast<size_t>(a.workspace_bytes), s);
+}
 
 hipError_t launch_spec_verify_static(const fl_spec_args& a, hipStream_t s) {
   if (spec_ws_bytes(a.batch) > SPEC_STATIC_BYTES) return hipErrorInvalidValue;  // (the caller checks first)
   void* p = nullptr;
   const hipError_t e = spec_static_scratch(&p);
   if (e != hipSuccess) return e;
-  return launch_spec_verify_on(a, p, s);
+  return launch_spec_verify_on(a, p, SPEC_STATIC_BYTES, s);
 }
 
-hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, hipStream_t s) {
+hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, size_t workspace_bytes, hipStream_t s) {
   const bool sliced = workspace != nullptr;
-  const SpecWs ws = sliced ? spec_ws(workspace, a.batch) : SpecWs{};
+  const SpecWs ws = sliced ? spec_ws(workspace, a.batch, workspace_bytes, a.vocab) : SpecWs{};
   const dim3 grid(static_cast<unsigned>(a.batch));
   auto run = [&](auto tag) {
     using D = decltype(tag);

@@ -44,7 +44,10 @@ class SpecPlan:
     The logits, draft ids and uniforms are read at launch time, so a decode
     loop may overwrite them in place between launches.  ``sliced`` spreads the
     residual draw of each rejected sequence over several work-groups (with a
-    workspace allocated here); ``sliced=False`` runs one work-group per
+    workspace allocated here; with ``cache_residual`` the workspace also
+    holds each rejected sequence's residual row, 4 bytes per vocabulary
+    entry, so the second pass and the draw read it instead of recomputing
+    both rows' probabilities); ``sliced=False`` runs one work-group per
     sequence; ``no_alloc=True`` runs the sliced path on the library's static
     device scratch (``fl_spec_verify_static``: no workspace, at most 4096
     sequences, plans that launch at the same time on one GPU race).  All give
@@ -54,7 +57,8 @@ class SpecPlan:
                  temperature: float = 1.0, top_k: Optional[int] = None, top_p: Optional[float] = None,
                  min_p: Optional[float] = None, softcap: float = 0.0, u_accept: Optional[torch.Tensor] = None,
                  u_resample: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
-                 return_ratio: bool = True, sliced: bool = True, no_alloc: bool = False):
+                 return_ratio: bool = True, sliced: bool = True, no_alloc: bool = False,
+                 cache_residual: bool = True):
         if target_logits.dim() != 3 or draft_logits.dim() != 3:
             raise ValueError("target_logits must be [B, K+1, V] and draft_logits [B, K, V]")
         B, K1, V = target_logits.shape
@@ -103,7 +107,10 @@ class SpecPlan:
             raise ValueError(f"no_alloc verifies at most {_lib.FL_SPEC_STATIC_MAX_BATCH} sequences, not {B}")
         sliced = sliced and not no_alloc
         nbytes = ctypes.c_size_t(0)
-        check(lib().fl_spec_workspace_bytes(B, ctypes.byref(nbytes)), "fl_spec_workspace_bytes")
+        if cache_residual:
+            check(lib().fl_spec_cache_workspace_bytes(B, V, ctypes.byref(nbytes)), "fl_spec_cache_workspace_bytes")
+        else:
+            check(lib().fl_spec_workspace_bytes(B, ctypes.byref(nbytes)), "fl_spec_workspace_bytes")
         self._ws = torch.empty(max(int(nbytes.value), 8), dtype=torch.uint8, device=dev) if sliced else None
         a.workspace = ptr(self._ws)
         a.workspace_bytes = int(nbytes.value) if sliced else 0

@@ -219,6 +219,21 @@ def test_spec_workspace_bytes_and_checks():
     assert L.fl_spec_verify(ctypes.byref(s), None) == _lib.FL_EINVAL
 
 
+def test_spec_cache_workspace_bytes():
+    """The cached workspace: the plain one padded to 16 bytes, then one float
+    row per sequence with the vocabulary rounded up to 8 entries."""
+    L = _lib.lib()
+    n, m = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    for b, v in ((32, 128256), (3, 1001), (1, 1), (512, 262144)):
+        assert L.fl_spec_workspace_bytes(b, ctypes.byref(n)) == _lib.FL_OK
+        assert L.fl_spec_cache_workspace_bytes(b, v, ctypes.byref(m)) == _lib.FL_OK
+        assert m.value == ((n.value + 15) // 16) * 16 + 4 * b * ((v + 7) // 8) * 8
+    assert L.fl_spec_cache_workspace_bytes(32, 0, ctypes.byref(m)) == _lib.FL_EINVAL
+    assert L.fl_spec_cache_workspace_bytes(32, _lib.FL_MAX_VOCAB_F32 + 1, ctypes.byref(m)) == _lib.FL_EINVAL
+    assert L.fl_spec_cache_workspace_bytes(-1, 10, ctypes.byref(m)) == _lib.FL_EINVAL
+    assert L.fl_spec_cache_workspace_bytes(4, 10, None) == _lib.FL_EINVAL
+
+
 def test_row_stats_argument_checks():
     """fl_row_stats rejects bad arguments before any launch (no GPU needed)."""
     L = _lib.lib()

@@ -110,10 +110,12 @@ def test_spec_disjoint_support_rejects_and_resamples_target():
     assert summ["MISMATCH"] == 0, verdicts
 
 
-@pytest.mark.parametrize("B,V,dtype", [(32, 128256, torch.float32), (12, 50000, torch.bfloat16), (3, 4099, torch.float32)])
+@pytest.mark.parametrize("B,V,dtype", [(32, 128256, torch.float32), (12, 50000, torch.bfloat16), (3, 4099, torch.float32),
+                                       (5, 32003, torch.bfloat16)])
 def test_spec_sliced_equals_single_workgroup(B, V, dtype):
-    """The residual draw spread over slices of the row pair (workspace path)
-    gives exactly the tokens of one work-group per sequence."""
+    """The residual draw spread over slices of the row pair (workspace path),
+    with the residual cached in the workspace and without, gives exactly the
+    tokens of one work-group per sequence."""
     from rl_project_amd.speculative import SpecPlan
     print(f"[spec sliced vs single] B={B} V={V} {dtype}", flush=True)
     g = torch.Generator().manual_seed(B + V)
@@ -124,17 +126,53 @@ def test_spec_sliced_equals_single_workgroup(B, V, dtype):
     ua = torch.rand(B, 5, generator=g).cuda()
     ur = torch.rand(B, generator=g).cuda()
     outs = []
-    for sliced in (True, False):
-        plan = SpecPlan(target, draft, ids, temperature=0.8, top_p=0.95, u_accept=ua, u_resample=ur, sliced=sliced)
+    for sliced, cache in ((True, True), (True, False), (False, False)):
+        plan = SpecPlan(target, draft, ids, temperature=0.8, top_p=0.95, u_accept=ua, u_resample=ur, sliced=sliced,
+                        cache_residual=cache)
         plan.launch()
         plan.launch()  # a second step on the same workspace
         torch.cuda.synchronize()
         assert bool(plan.status_ok().all())
         outs.append((plan.n_accepted.clone(), plan.tokens.clone(), plan.ratio.clone()))
-    (n1, t1, r1), (n2, t2, r2) = outs
+    n1, t1, r1 = outs[0]
     assert int((n1 < 5).sum()) > 0, "no rejection exercised"
+    for n2, t2, r2 in outs[1:]:
+        assert torch.equal(n1, n2) and torch.equal(t1, t2)
+        assert torch.equal(torch.nan_to_num(r1, nan=-1.0), torch.nan_to_num(r2, nan=-1.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_spec_cached_residual_all_zero_draws_from_target(dtype):
+    """Target and draft rows equal: every residual max(0, p - q) is zero, so
+    the draw falls back to p (the cached path reads the rows again).  Drafts
+    outside the top-p nucleus (p = 0) are rejected; the cached and uncached
+    workspaces give the same tokens, all inside the nucleus."""
+    from rl_project_amd.speculative import SpecPlan
+    B, K, V = 6, 3, 40000
+    print(f"[spec cached zero residual] B={B} V={V} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    target = (2.0 * torch.randn(B, K + 1, V, generator=g)).to(dtype).cuda()
+    draft = target[:, :K].clone()
+    ids = target[:, :K].float().argmin(-1)          # the least likely token: outside top-p 0.5
+    ua = torch.rand(B, K, generator=g).cuda()
+    ur = torch.rand(B, generator=g).cuda()
+    outs = []
+    for cache in (True, False):
+        plan = SpecPlan(target, draft, ids, temperature=0.8, top_p=0.5, u_accept=ua, u_resample=ur, cache_residual=cache)
+        plan.launch()
+        torch.cuda.synchronize()
+        assert bool(plan.status_ok().all())
+        outs.append((plan.n_accepted.clone(), plan.tokens.clone()))
+    (n1, t1), (n2, t2) = outs
+    assert bool((n1 == 0).all()), n1
     assert torch.equal(n1, n2) and torch.equal(t1, t2)
-    assert torch.equal(torch.nan_to_num(r1, nan=-1.0), torch.nan_to_num(r2, nan=-1.0))
+    # the first token is a draw from p: among the top-p 0.5 survivors of row 0
+    y = (target[:, 0].float() / 0.8)
+    for b in range(B):
+        probs = torch.softmax(y[b].double(), -1)
+        order = torch.argsort(probs, descending=True)
+        kept = order[: int((torch.cumsum(probs[order], 0) < 0.5).sum()) + 8]
+        assert int(t1[b, 0]) in set(kept.tolist())
 
 
 class _ToyMTP(torch.nn.Module):
