@@ -17,17 +17,17 @@
 
 // Phase timestamps for kernel tuning builds (-DFL_PHASE_TIMES): thread 0 of
 // each of the first 1024 work-groups records the constant-rate wall clock at
-// each FL_MARK(n), n < 16, in slot 16 * blockIdx.x + n.
+// each FL_MARK(n), n < 32, in slot 32 * blockIdx.x + n.
 #ifdef FL_PHASE_TIMES
-#define FL_PHASE_SLOTS (16 * 1024)
+#define FL_PHASE_SLOTS (32 * 1024)
 static __device__ uint64_t fl_phase_ts[FL_PHASE_SLOTS];
 #ifndef FL_MARK_MASK
-#define FL_MARK_MASK 0xFFFF  // marks recorded (bit n: FL_MARK(n)); fewer marks, fewer spills
+#define FL_MARK_MASK 0xFFFFFFFFu  // marks recorded (bit n: FL_MARK(n)); fewer marks, fewer spills
 #endif
 #define FL_MARK(n)                                                              \
   do {                                                                          \
     if (((FL_MARK_MASK >> (n)) & 1) && threadIdx.x == 0 && blockIdx.x < 1024)   \
-      fl_phase_ts[blockIdx.x * 16 + (n)] = wall_clock64();                      \
+      fl_phase_ts[blockIdx.x * 32 + (n)] = wall_clock64();                      \
   } while (0)
 #else
 #define FL_MARK(n) \
