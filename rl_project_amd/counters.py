@@ -2,6 +2,8 @@
 
     python -m rl_project_amd.counters KERNEL ELEMENTS DIR [DIR ...]
     python -m rl_project_amd.counters --traffic KERNEL ALG_BYTES FETCH_DIR WRITE_DIR CAL_FETCH_DIR CAL_WRITE_DIR
+    python -m rl_project_amd.counters --traffic-step STEP_KERNEL ALG_BYTES FETCH_DIR WRITE_DIR CAL_FETCH_DIR
+                                      CAL_WRITE_DIR KERNEL [KERNEL ...]
 
 reads every ``*counter_collection.csv`` under the directories (one
 directory per counter pass: a pass may hold at most 8 SQ, 4 TCC, 2 TA/TD and
@@ -129,7 +131,34 @@ def traffic(kernel: str, alg_bytes: float, fetch_dir: str, write_dir: str, cal_f
         f"traffic_over_algorithmic: {t / alg_bytes:.3f}"])
 
 
+def traffic_step(step_kernel: str, alg_bytes: float, fetch_dir: str, write_dir: str, cal_fetch_dir: str,
+                 cal_write_dir: str, kernels: List[str], cal_kernel: str = "neg_kernel",
+                 cal_bytes: float = 256.0 * (1 << 20)) -> str:
+    """HBM bytes per step of a workload made of several kernels: for each
+    kernel name fragment in ``kernels``, its median FETCH_SIZE / WRITE_SIZE
+    per dispatch (scaled as in ``traffic``) times its dispatches per step, a
+    step being one dispatch of ``step_kernel``."""
+    med = lambda d, k, n: statistics.median(load([d], k)[n])  # noqa: E731
+    fs = cal_bytes / 1024.0 / med(cal_fetch_dir, cal_kernel, "FETCH_SIZE")
+    ws = cal_bytes / 1024.0 / med(cal_write_dir, cal_kernel, "WRITE_SIZE")
+    steps = len(load([fetch_dir], step_kernel)["FETCH_SIZE"])
+    lines, total = [f"fetch_scale: {fs:.5f}", f"write_scale: {ws:.5f}"], 0.0
+    for k in kernels:
+        fv, wv = load([fetch_dir], k)["FETCH_SIZE"], load([write_dir], k)["WRITE_SIZE"]
+        per_step = len(fv) / steps
+        b = 1024.0 * (statistics.median(fv) * fs + statistics.median(wv) * ws) * per_step
+        total += b
+        lines.append(f"{k}: fetch_kib_median {statistics.median(fv):.1f} write_kib_median {statistics.median(wv):.1f} "
+                     f"launches_per_step {per_step:.2f} bytes_per_step {b:.0f}")
+    lines += [f"algorithmic_bytes_per_step: {alg_bytes:.0f}", f"traffic_bytes_per_step: {total:.0f}",
+              f"traffic_over_algorithmic: {total / alg_bytes:.3f}"]
+    return "\n".join(lines)
+
+
 def main(argv: List[str]) -> int:
+    if argv and argv[0] == "--traffic-step" and len(argv) >= 9:
+        print(traffic_step(argv[1], float(argv[2]), *argv[3:7], kernels=argv[7:]))
+        return 0
     if argv and argv[0] == "--traffic" and len(argv) == 7:
         print(traffic(argv[1], float(argv[2]), *argv[3:7]))
         return 0
