@@ -539,14 +539,17 @@ __device__ __forceinline__ int fbin(float y, float c) {
 }
 // Upper bound of bin b's values (up to rounding).
 __device__ __forceinline__ float fub(int b, float c) { return c - static_cast<float>(b) * (1.0f / BPU); }
-// round(exp(y - ub_b) * 2^26) for y in bin b; y - ub_b lies in about
-// [-1/64, 0], where the degree-4 Taylor polynomial is exact to 1e-11, and
-// t * 2^26 < 2^27 is an integer (t has 24 significant bits).  The last bin
-// adds no mass: its values lie more than 40 below the anchor, so their
-// weights are below e^-40 of the largest.
+// round(exp(y - ub_b) * 2^26) for y in bin b.  With u = (c - y) * 64, whose
+// integer part is b (fbin), y - ub_b = -fract(u) / 64 lies in (-1/64, 0]; the
+// degree-4 Taylor polynomial of exp(-f / 64) in f = fract(u) is exact to
+// 1e-11 there (one v_fract_f32 and four FMAs per value; rebuilding the bound
+// from b took four more), and t * 2^26 < 2^27 is an integer (t has 24
+// significant bits).  The last bin adds no mass: its values lie more than 40
+// below the anchor, so their weights are below e^-40 of the largest.
 __device__ __forceinline__ uint32_t fterm(float y, int b, float c) {
-  const float d = fminf(y - fub(b, c), 0.0625f);
-  const float t = fmaf(d, fmaf(d, fmaf(d, fmaf(d, 1.0f / 24.0f, 1.0f / 6.0f), 0.5f), 1.0f), 1.0f);
+  const float f = __builtin_amdgcn_fractf((c - y) * BPU);
+  const float t = fmaf(f, fmaf(f, fmaf(f, fmaf(f, 1.0f / 402653184.0f, -1.0f / 1572864.0f), 1.0f / 8192.0f),
+                               -1.0f / 64.0f), 1.0f);
   return b == NBF - 1 ? 0u : static_cast<uint32_t>(t * 67108864.0f);
 }
 // Mass in 2^-45 fixed point relative to M of term sum F (2^-26 units) in bin b:
