@@ -544,19 +544,22 @@ __device__ __forceinline__ float fub(int b, float c) { return c - static_cast<fl
 // degree-4 Taylor polynomial of exp(-f / 64) in f = fract(u) is exact to
 // 1e-11 there (one v_fract_f32 and four FMAs per value; rebuilding the bound
 // from b took four more), and t * 2^26 < 2^27 is an integer (t has 24
-// significant bits).  The last bin adds no mass: its values lie more than 40
-// below the anchor, so their weights are below e^-40 of the largest.
-__device__ __forceinline__ uint32_t fterm(float y, int b, float c) {
+// significant bits; at most 2^18 of them fit the bin word's 45-bit field).
+// Terms of the last bin are summed like the others (a value there is finite
+// or -inf, whose fraction is NaN and converts to 0) and dropped by fmass.
+__device__ __forceinline__ uint32_t fterm(float y, float c) {
   const float f = __builtin_amdgcn_fractf((c - y) * BPU);
   const float t = fmaf(f, fmaf(f, fmaf(f, fmaf(f, 1.0f / 402653184.0f, -1.0f / 1572864.0f), 1.0f / 8192.0f),
                                -1.0f / 64.0f), 1.0f);
-  return b == NBF - 1 ? 0u : static_cast<uint32_t>(t * 67108864.0f);
+  return static_cast<uint32_t>(t * 67108864.0f);
 }
 // Mass in 2^-45 fixed point relative to M of term sum F (2^-26 units) in bin b:
 // round(F * exp(ub_b - M) * 2^19).  Bin totals and in-bin prefixes both use it,
-// so the prefixes of a bin end exactly at its total.
+// so the prefixes of a bin end exactly at its total.  The last bin adds no
+// mass: its values lie more than 40 below the anchor, so their weights are
+// below e^-40 of the largest.
 __device__ __forceinline__ uint64_t fmass(uint64_t F, int b, float c, float M) {
-  if (F == 0) return 0;
+  if (F == 0 || b == NBF - 1) return 0;
   const double g = exp(static_cast<double>(fub(b, c)) - static_cast<double>(M)) * 524288.0;
   return static_cast<uint64_t>(static_cast<double>(F) * g + 0.5);
 }
@@ -1092,7 +1095,7 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
     km = max(km, ok ? f32_key(y) : 0u);
     nfin += (ok && y > -__builtin_inff()) ? 1u : 0u;
     const int b = fbin(y, c);
-    const uint64_t w = (1ull << CNT_SH) | fterm(y, b, c);
+    const uint64_t w = (1ull << CNT_SH) | fterm(y, c);
     atomicAdd(reinterpret_cast<unsigned long long*>(&sh.acc[ok ? b : NBF]),
               static_cast<unsigned long long>(ok ? w : 0ull));
   };
@@ -1110,7 +1113,7 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int b = fbin(y[e], c);
-        const uint64_t w = (1ull << CNT_SH) | fterm(y[e], b, c);
+        const uint64_t w = (1ull << CNT_SH) | fterm(y[e], c);
         atomicAdd(reinterpret_cast<unsigned long long*>(&sh.acc[b]), static_cast<unsigned long long>(w));
       }
     } else {
@@ -1516,7 +1519,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
         if (i < n) {
           const float y = f32_of_key(static_cast<uint32_t>(sh.cand[i] >> 32));
           bb[j] = fbin(y, c);
-          f[j] = fterm(y, bb[j], c);
+          f[j] = fterm(y, c);
           ls += f[j];
         }
       }
