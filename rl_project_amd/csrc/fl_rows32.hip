@@ -547,11 +547,15 @@ __device__ __forceinline__ float fub(int b, float c) { return c - static_cast<fl
 // significant bits; at most 2^18 of them fit the bin word's 45-bit field).
 // Terms of the last bin are summed like the others (a value there is finite
 // or -inf, whose fraction is NaN and converts to 0) and dropped by fmass.
+// (The coefficients carry the factor 2^26: scaling by a power of two commutes
+// with each rounding of the Horner chain, so this is t * 2^26 exactly.)
 __device__ __forceinline__ uint32_t fterm(float y, float c) {
   const float f = __builtin_amdgcn_fractf((c - y) * BPU);
-  const float t = fmaf(f, fmaf(f, fmaf(f, fmaf(f, 1.0f / 402653184.0f, -1.0f / 1572864.0f), 1.0f / 8192.0f),
-                               -1.0f / 64.0f), 1.0f);
-  return static_cast<uint32_t>(t * 67108864.0f);
+  const float t26 = fmaf(f, fmaf(f, fmaf(f, fmaf(f, 67108864.0f / 402653184.0f, -67108864.0f / 1572864.0f),
+                                               67108864.0f / 8192.0f),
+                                 -67108864.0f / 64.0f),
+                         67108864.0f);
+  return static_cast<uint32_t>(t26);
 }
 // Mass in 2^-45 fixed point relative to M of term sum F (2^-26 units) in bin b:
 // round(F * exp(ub_b - M) * 2^19).  Bin totals and in-bin prefixes both use it,
