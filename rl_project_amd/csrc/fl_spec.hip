@@ -108,10 +108,10 @@ struct SharedSpec {
 
 // Accept walk of sequence b (one wave): ratio = min(1, p(d)/(q(d)+1e-10))
 // in the logits' dtype (:63), accept iff u_accept < ratio (:65).  Writes the
-// ratios and the accepted drafts; returns the accepted count, *rej = whether
-// a draft was rejected.
+// ratios and the accepted drafts when `write`; returns the accepted count,
+// *rej = whether a draft was rejected.
 template <class D>
-__device__ int accept_walk(const fl_spec_args& a, int64_t b, bool* rej) {
+__device__ int accept_walk(const fl_spec_args& a, int64_t b, bool* rej, bool write = true) {
   // Called by one whole wave: lane l evaluates positions l, l + 64, ... in
   // parallel (their loads in flight together); the first position whose
   // draw fails the ratio ends the walk, as the sequential rule has it.
@@ -144,14 +144,14 @@ __device__ int accept_walk(const fl_spec_args& a, int64_t b, bool* rej) {
     }
     const uint64_t fail = __ballot(i < K && !acc);
     const int64_t f = fail ? i0 + __ffsll(static_cast<unsigned long long>(fail)) - 1 : K;
-    if (i < K) {
+    if (write && i < K) {
       if (a.out_ratio) a.out_ratio[b * K + i] = i <= f ? ratio : __builtin_nanf("");
       if (i < f) a.out_tokens[b * (K + 1) + i] = d;
     }
     n = f;
   }
   // (positions of rounds after the rejecting one: no ratio)
-  if (a.out_ratio && n < K)
+  if (write && a.out_ratio && n < K)
     for (int64_t i = (n / WAVE + 1) * WAVE + lane; i < K; i += WAVE) a.out_ratio[b * K + i] = __builtin_nanf("");
   *rej = n < K;
   return static_cast<int>(n);
@@ -518,26 +518,38 @@ __global__ __launch_bounds__(NT) void k_spec_verify(const fl_spec_args a) {
 }
 
 // ---------------------------------------------------------------- sliced path
-// 1. accept walk per sequence; a sequence with no rejection is finished here
-template <class D>
-__global__ __launch_bounds__(WAVE) void k_spec_accept(const fl_spec_args a, SpecWs ws) {
-  const int64_t b = blockIdx.x;
-  bool rej;
-  const int n = accept_walk<D>(a, b, &rej);
-  if (threadIdx.x != 0) return;
-  ws.state[b] = rej ? n : -1;
-  if (rej) a.out_n_accepted[b] = n;
-  else write_tail(a, b, n, a.bonus_token[b * (a.k + 1) + a.k]);
-}
-
-// 2. per slice of the rejected position's row pair: sum(r) (PASS2 false), or
-//    the sum of the weights (PASS2 true, after every slice's sum(r))
+// 1. per slice of the rejected position's row pair: sum(r) (PASS2 false), or
+//    the sum of the weights (PASS2 true, after every slice's sum(r)).  The
+//    first pass starts with the accept walk, in every slice's work-group (a
+//    few gathers per sequence, served by L2 after the first): slice 0 writes
+//    the walk's outputs, the sequence's state for the later launches and,
+//    when every draft is accepted, its tokens; a separate launch for the walk
+//    cost 5.5 us of the verify.
 template <class D, bool PASS2>
 __global__ __launch_bounds__(NT_PART) void k_spec_part(const fl_spec_args a, SpecWs ws) {
   __shared__ uint64_t red[NT_PART / WAVE];
+  __shared__ int32_t pos_sh;
   const int64_t b = blockIdx.y;
   const int s = blockIdx.x;
-  const int pos = ws.state[b];
+  int pos;
+  if constexpr (!PASS2) {
+    if (threadIdx.x < WAVE) {
+      bool rej;
+      const int n = accept_walk<D>(a, b, &rej, s == 0);
+      if (threadIdx.x == 0) {
+        pos_sh = rej ? n : -1;
+        if (s == 0) {
+          ws.state[b] = rej ? n : -1;
+          if (rej) a.out_n_accepted[b] = n;
+          else write_tail(a, b, n, a.bonus_token[b * (a.k + 1) + a.k]);
+        }
+      }
+    }
+    __syncthreads();
+    pos = pos_sh;
+  } else {
+    pos = ws.state[b];
+  }
   if (pos < 0) return;
   const PairRows<D> R(a, b, pos);
   const int cps = (R.nch + ws.S - 1) / ws.S;
@@ -563,7 +575,7 @@ __global__ __launch_bounds__(NT_PART) void k_spec_part(const fl_spec_args a, Spe
   if (threadIdx.x == 0) (PASS2 ? ws.part2 : ws.part1)[b * ws.S + s] = v;
 }
 
-// 3. the slice holding floor(u * W), then the member inside it
+// 2. the slice holding floor(u * W), then the member inside it
 template <class D>
 __global__ __launch_bounds__(NT) void k_spec_pick(const fl_spec_args a, SpecWs ws) {
   __shared__ SharedSpec sh;
@@ -606,7 +618,7 @@ size_t spec_cache_workspace_bytes(int64_t batch, int64_t vocab) { return spec_ca
 // The sliced path's workspace for up to FL_SPEC_STATIC_MAX_BATCH sequences
 // (20 bytes a sequence at 4096 of them; at most 40 KiB below 2048), one copy on
 // each GPU the library runs on, held until the process ends.  Every byte a
-// call reads was written earlier in the same call (the accept kernel writes
+// call reads was written earlier in the same call (the first slice pass writes
 // each sequence's state, the slice kernels each part they later read), so
 // nothing is cleared between calls; calls that overlap on one GPU race.
 constexpr size_t SPEC_STATIC_BYTES = 81920;
@@ -663,7 +675,6 @@ hipError_t launch_spec_verify_on(const fl_spec_args& a, void* workspace, size_t 
       return;
     }
     const dim3 pgrid(static_cast<unsigned>(ws.S), static_cast<unsigned>(a.batch));
-    hipLaunchKernelGGL(k_spec_accept<D>, grid, dim3(WAVE), 0, s, a, ws);
     hipLaunchKernelGGL((k_spec_part<D, false>), pgrid, dim3(NT_PART), 0, s, a, ws);
     hipLaunchKernelGGL((k_spec_part<D, true>), pgrid, dim3(NT_PART), 0, s, a, ws);
     hipLaunchKernelGGL(k_spec_pick<D>, grid, dim3(NT), 0, s, a, ws);
