@@ -271,12 +271,16 @@ __device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f, in
   }
 }
 
-// f(c, xs, hb) for every chunk c of the row: its raw logits and history bits.
+// f(c, xs, hb) for every chunk c of the row, in groups of 4 NT chunks from the
+// last group to the first: its raw logits and history bits.
 template <class F>
 __device__ __forceinline__ void row_chunks_raw(const Src& S, const Xform& X, F&& f) {
   const int tid = threadIdx.x;
   const int nch = X.nch;
-  for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
+  // (last chunks first: read 1 went first to last, so the bytes it read most
+  // recently, the likeliest still in the caches, are read again first;
+  // speculative rows 2.4 us faster per step, A/B on one box)
+  for (int c0 = nch > 0 ? ((nch - 1) / (4 * NT)) * (4 * NT) : -1; c0 >= 0; c0 -= 4 * NT) {
     float4 q[4];
     S.chunks(c0, q);
 #pragma unroll
