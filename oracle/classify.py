@@ -32,6 +32,11 @@ oracle's, except for
                             (``_softcap_selection_near``); greedy picks must be able to
                             win the first-index argmax under ``RK``
                             (``greedy_near``);
+                 soft-cap   a soft-capped row's mask and draw judged as the
+                            oracle's filters and selection on the kernel's
+                            own unfiltered values, when those are the
+                            oracle's within a few units of the dtype
+                            (``_softcap_on_kernel_values``);
                  speculative  accept ratios and residual / bonus draws
                             with the oracle's filtered rows and, where a
                             row's top-p cut is open (``_top_p_count_range``),
@@ -133,23 +138,16 @@ def _top_p_count_range(y: np.ndarray, surv: np.ndarray, grp: np.ndarray, top_p: 
     U = np.abs(c_ref - c_k) + np.cumsum(amb) + 1e-12
     pos = np.nonzero(np.isin(order.numpy(), grp))[0]
 
-    def removed(c, pp):
-        return bool(_rn(_rn(np.float64(c), dt) - pp, dt) >= t)
-
-    lo_n = hi_n = 0
-    lo_done = hi_done = False
-    for j in pos:
-        outcomes = [removed(c_ref[j] + s1 * U[j], ps[j] + s2 * amb[j]) for s1 in (-1, 0, 1) for s2 in (-1, 0, 1)]
-        if not lo_done:
-            if not any(outcomes):
-                lo_n += 1
-            else:
-                lo_done = True
-        if not hi_done:
-            if not all(outcomes):
-                hi_n += 1
-            else:
-                hi_done = True
+    # the removal test of every member at the 9 corners of its doubt
+    s1, s2 = np.repeat([-1.0, 0.0, 1.0], 3)[:, None], np.tile([-1.0, 0.0, 1.0], 3)[:, None]
+    c = c_ref[pos][None, :] + s1 * U[pos][None, :]
+    pp = ps[pos][None, :] + s2 * amb[pos][None, :]
+    rem = _rn(_rn(c, dt) - pp, dt) >= t
+    some, every = rem.any(axis=0), rem.all(axis=0)
+    # kept members form a prefix: certain kept up to the first member that
+    # may be removed, possibly kept up to the first one certainly removed
+    lo_n = int(np.argmax(some)) if some.any() else int(pos.size)
+    hi_n = int(np.argmax(every)) if every.any() else int(pos.size)
     j0 = pos[0] if pos.size else 0
     return lo_n, hi_n, float(c_ref[j0] - ps[j0]) if pos.size else 0.0
 
@@ -230,17 +228,38 @@ def _min_p_survivor_sets(pre_minp: np.ndarray, probs: np.ndarray, min_p: float, 
 
 def classify_row(x: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tensor, ref_tok: int,
                  got_keep: Optional[torch.Tensor], got_tok: Optional[int], softcap: float = 0.0,
-                 rel: float = REL, got_values: Optional[torch.Tensor] = None) -> RowVerdict:
+                 rel: float = REL, got_values: Optional[torch.Tensor] = None,
+                 got_all_values: Optional[torch.Tensor] = None) -> RowVerdict:
     """Classify one row.  ``x``: the input row [V]; ``ref_keep``/``got_keep``:
     bool [V] keep masks (``got_keep`` may be None to check the token only).
     ``got_values``: the kernel's filtered values of the row (-inf outside its
-    mask), used only for soft-capped rows (see ``_softcap_selection_near``)."""
-    dt = x.dtype
+    mask), used only for soft-capped rows (see ``_softcap_selection_near``).
+    ``got_all_values``: the kernel's unfiltered values of the row (soft-cap,
+    penalty and temperature applied, nothing removed), used only for
+    soft-capped rows (see ``_softcap_on_kernel_values``)."""
     same_mask = got_keep is None or bool(torch.equal(ref_keep, got_keep))
     if same_mask and (got_tok is None or got_tok == ref_tok):
         return RowVerdict("EXACT")
     hist = p.history if p.repetition_penalty != 1.0 else None
     y_t = O.pre_filter_values(x[None], p.temperature, p.repetition_penalty, hist, softcap)[0]
+    verdict = _classify_on(y_t, p, u, ref_keep, ref_tok, got_keep, got_tok, softcap, got_values)
+    if verdict.kind == "MISMATCH" and softcap > 0 and got_all_values is not None:
+        alt = _softcap_on_kernel_values(y_t, got_all_values, p, u, got_keep, got_tok, softcap, got_values)
+        if alt is not None:
+            return alt
+    return verdict
+
+
+def _classify_on(y_t: torch.Tensor, p: O.RowParams, u: float, ref_keep: torch.Tensor, ref_tok: int,
+                 got_keep: Optional[torch.Tensor], got_tok: Optional[int], softcap: float,
+                 got_values: Optional[torch.Tensor]) -> RowVerdict:
+    """``classify_row`` on given pre-filter values ``y_t`` [V] (the values the
+    filters compare), with ``ref_keep`` / ``ref_tok`` the oracle's result on
+    them."""
+    dt = y_t.dtype
+    same_mask = got_keep is None or bool(torch.equal(ref_keep, got_keep))
+    if same_mask and (got_tok is None or got_tok == ref_tok):
+        return RowVerdict("EXACT")
     y = y_t.double().numpy()
     V = y.size
     verdict = RowVerdict("TIE")
@@ -398,6 +417,48 @@ def selection_near(filt: torch.Tensor, u: float, got_tok: int) -> tuple:
 
 
 SOFTCAP_ULPS = {torch.float32: 8, torch.bfloat16: 2, torch.float16: 2}
+
+
+def _softcap_on_kernel_values(y_t: torch.Tensor, got_all_values: torch.Tensor, p: O.RowParams, u: float,
+                              got_keep: Optional[torch.Tensor], got_tok: Optional[int], softcap: float,
+                              got_values: Optional[torch.Tensor]) -> Optional[RowVerdict]:
+    """A soft-capped row whose mask or draw differs from the oracle's because
+    the kernel's tanh rounded values to a neighbouring representable number:
+    the soft-cap flattens large values into a few value groups at and next
+    to the cap, so one unit moves an element from one group to the next,
+    across a top-p or min-p cut or past the draw.  NEAR when the kernel's
+    unfiltered values ``got_all_values`` are the oracle's ``y_t`` within
+    ``SOFTCAP_ULPS`` units of the dtype (the same elements -inf) and the
+    kernel's mask and token are what the oracle's own filters and selection
+    give on those values, up to TIE / NEAR / CONSEQ; None otherwise."""
+    dt = y_t.dtype
+    g = got_all_values.to(dt)
+    yn, gn = y_t.double().numpy(), g.double().numpy()
+    fin = np.isfinite(yn)
+    if not np.array_equal(fin, np.isfinite(gn)) or not np.array_equal(yn[~fin], gn[~fin]):
+        return None
+    mant = {torch.float32: 23, torch.bfloat16: 7, torch.float16: 10}[dt]
+    yk, gk = yn[fin], gn[fin]
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(yk), torch.finfo(dt).tiny))) - mant)
+    units = np.abs(gk - yk) / ulp
+    if yk.size and float(units.max()) > SOFTCAP_ULPS[dt]:
+        return None
+    stage = g[None].clone()
+    stage = O._top_k(stage, p.top_k or None)
+    stage = O._min_p(stage, p.min_p or None)
+    stage = O._top_p(stage, p.top_p, True)
+    keep = ~torch.isneginf(stage[0])
+    tok = O.select_token(stage[0], u, p.temperature)
+    v = _classify_on(g, p, u, keep, tok, got_keep, got_tok, softcap, got_values)
+    if v.kind == "MISMATCH":
+        return None
+    moved = int(np.count_nonzero(units))
+    out = RowVerdict("NEAR", details=[f"on the kernel's soft-capped values ({moved} differ from the oracle's, "
+                                      f"at most {float(units.max()) if yk.size else 0.0:.0f} units): {v.kind}"]
+                      + v.details)
+    rel_diff = np.abs(gk - yk) / np.maximum(np.abs(yk), torch.finfo(dt).tiny)
+    out.margin = max(v.margin, float(rel_diff.max()) if yk.size else 0.0)
+    return out
 
 
 def _softcap_selection_near(y: np.ndarray, got_values: torch.Tensor, keep: np.ndarray, u: float, got_tok: int,

@@ -358,6 +358,61 @@ def test_softcap_saturated_draw_on_the_kernels_values():
     assert v.kind == "MISMATCH", v.details
 
 
+def _filters_on(vals, p, u):
+    """The oracle's filters and selection applied to given pre-filter values."""
+    st = vals[None].clone()
+    st = O._top_k(st, p.top_k or None)
+    st = O._min_p(st, p.min_p or None)
+    st = O._top_p(st, p.top_p, True)
+    return ~torch.isneginf(st[0]), O.select_token(st[0], u, p.temperature)
+
+
+def test_softcap_mask_on_the_kernels_values():
+    """Row 0 of the sweep case of seed 401310: float32, V 151936, x ~ N(0,
+    60^2), cap 5, T 1.5, top-p 0.5, min-p 0.3.  34524 values sit at the cap
+    and the top-p cut falls inside the value group one unit below it.
+    tanh(x / 5) of the two smallest capped x (45.0543, 45.0545) lies next to
+    the midpoint between 1 and the float below it, and a kernel's tanh
+    rounded both down: they join the cut group, one of them lands past the
+    cut, and the token moves.  With the kernel's unfiltered values (the
+    oracle's, those two moved one unit down) the mask and token that the
+    oracle's filters give on them are NEAR, and without them MISMATCH; the
+    whole cut group kept, the next token of the order, or the two values
+    moved 20 units are MISMATCH."""
+    from tests.helpers import row_params, sweep_case
+
+    w, _ = sweep_case(401310)
+    x, p, u, cap = w.logits[0], row_params(w, 0), float(w.uniforms[0]), w.softcap
+    r, keep, y = _oracle(x, p, u, softcap=cap)
+    at_cap = torch.nonzero(y == y.max()).flatten()
+    low2 = at_cap[torch.argsort(x[at_cap])[:2]]
+    moved = y.clone()
+    moved[low2] = torch.nextafter(moved[low2], torch.tensor(float("-inf")))
+    gkeep, gtok = _filters_on(moved, p, u)
+    assert not torch.equal(gkeep, keep) and gtok != r.token
+    assert _kind(x, p, u, keep, r.token, gkeep, gtok, softcap=cap).kind == "MISMATCH"
+    v = C.classify_row(x, p, u, keep, r.token, gkeep, gtok, softcap=cap, got_all_values=moved)
+    assert v.kind == "NEAR", v.details
+    # the cut group kept whole
+    cut = float(moved[gkeep].min())
+    whole = gkeep | (moved == cut)
+    assert not torch.equal(whole, gkeep)
+    wtok = O.select_token(torch.where(whole, moved, torch.tensor(float("-inf"))), u, p.temperature)
+    v = C.classify_row(x, p, u, keep, r.token, whole, wtok, softcap=cap, got_all_values=moved)
+    assert v.kind == "MISMATCH", v.details
+    # the next token of the order on the kernel's mask
+    order = O.selection_order(torch.where(gkeep, moved, torch.tensor(float("-inf")))).tolist()
+    nxt = order[order.index(gtok) + 1]
+    v = C.classify_row(x, p, u, keep, r.token, gkeep, nxt, softcap=cap, got_all_values=moved)
+    assert v.kind == "MISMATCH", v.details
+    # values 20 units away
+    far = y.clone()
+    far[low2] = far[low2] - 20 * 2.0 ** -22   # one unit of [2, 4) is 2^-22
+    fkeep, ftok = _filters_on(far, p, u)
+    v = C.classify_row(x, p, u, keep, r.token, fkeep, ftok, softcap=cap, got_all_values=far)
+    assert v.kind == "MISMATCH", v.details
+
+
 def _kernel16_min_p_top_p(y: torch.Tensor, min_p: float, top_p: float):
     """CPU model of the 16-bit row kernel's min-p and top-p arithmetic on the
     distinct values of a row (rl_project_amd/csrc/fl_rows16.hip, the top-k /

@@ -49,3 +49,36 @@ def test_sweep_seed_202175_f32_top_p_over_soft_capped_top_k_survivors():
     want = torch.zeros_like(keep[0])
     want[order[:901]] = True
     assert torch.equal(keep[ok_rows.index(2)], want)
+
+
+def test_sweep_seed_401310_f32_top_p_next_to_the_soft_cap():
+    """float32, V=151936, soft-cap 5, x ~ N(0, 60^2) (8 rows).  Row 0 (T 1.5,
+    top-p 0.5, min-p 0.3): 34524 values sit at the cap and the top-p cut
+    falls inside the group one unit below it.  The two smallest capped
+    inputs (45.0543, 45.0545, indices 24710 and 29445) have tanh(x / 5) next
+    to the midpoint between 1 and the float below it; the kernel rounds both
+    down, they join the cut group, one lands past the cut and the token
+    moves.  The kernel's mask and token must be the oracle's filters and
+    draw on the kernel's own unfiltered values (within 8 units of the
+    oracle's), so every row classifies without MISMATCH."""
+    from oracle import sampler_oracle as O
+    from tests.helpers import row_params, unfiltered_values
+
+    w, ok_rows, st, summ, verdicts, toks, keep = run_sweep_case(401310)
+    print(f"seed 401310: status {st.tolist()} {summ}", flush=True)
+    assert summ["MISMATCH"] == 0, [v.details[:3] for v in verdicts if not v.ok]
+    assert 0 in ok_rows
+    wd = w.to("cuda")
+    kw = wd.kwargs()
+    kw.pop("uniforms")
+    allv = unfiltered_values(wd.logits, kw).cpu()
+    p = row_params(w, 0)
+    y = O.pre_filter_values(w.logits[0][None], p.temperature, p.repetition_penalty, None, w.softcap)[0]
+    # the two values below the cap on the kernel, at the cap in the oracle
+    assert torch.equal(torch.nonzero((y == y.max()) & (allv[0] < y.max())).flatten(),
+                       torch.tensor([24710, 29445]))
+    st_ = allv[0][None].clone()
+    st_ = O._min_p(st_, p.min_p)
+    st_ = O._top_p(st_, p.top_p, True)
+    assert torch.equal(keep[ok_rows.index(0)], ~torch.isneginf(st_[0]))
+    assert int(toks[0]) == O.select_token(st_[0], float(w.uniforms[0]), p.temperature)
