@@ -158,11 +158,13 @@ struct Src {
   // aligned row (every iteration of a streaming loop but the last), one
   // uniform test covers them and each is one 16-byte load; a test per chunk
   // would put a branch around every load and make the wave wait for all U
-  // loads before it uses the first.
+  // loads before it uses the first.  A row of whole chunks (V a multiple of
+  // 4) takes 16-byte loads throughout: a chunk past its end lies wholly
+  // outside the buffer's range and reads zeros.
   template <int U>
   __device__ __forceinline__ void chunks(int c0, float4 (&q)[U]) const {
     const int tid = threadIdx.x;
-    if (aligned && c0 + U * NT <= nfull) {
+    if (aligned && (c0 + U * NT <= nfull || 4 * nfull == V)) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint4 v = buf_load16(rs, 16u * static_cast<uint32_t>(c0 + u * NT + tid), 0u);
@@ -1657,6 +1659,14 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const float RP = a.rep_penalty[b];
   const float U_in = select ? a.uniforms[a.uniform_div > 1 ? b / a.uniform_div : b] : 0.0f;
   const int H_in = a.hist_ids ? a.hist_len[b] : 0;
+  // Each thread's first history id, requested by row stride before the row's
+  // length is known, so that the id arrives with the parameters rather than
+  // one memory round trip after them (the temperature array stands in when
+  // there is no per-row id list, keeping the load unconditional).
+  const bool hist_rows = a.hist_ids != nullptr && a.hist_ld > 0;
+  const int32_t* hid = a.hist_ids ? a.hist_ids + b * a.hist_ld : nullptr;
+  const int32_t hid0 = (hist_rows ? hid : reinterpret_cast<const int32_t*>(a.temperature))
+      [hist_rows ? min(tid, static_cast<int>(min(a.hist_ld, static_cast<int64_t>(NT))) - 1) : 0];
   const float U = select ? fminf(fmaxf(U_in, 0.0f), 0.99999994f) : 0.0f;
   const bool hist_too_long = H_in > FL_MAX_HISTORY;
   const int H = (a.hist_ids != nullptr && RP != 1.0f && !hist_too_long) ? max(H_in, 0) : 0;
@@ -1687,9 +1697,8 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   }
   __syncthreads();
   if (pen) {
-    const int32_t* hid = a.hist_ids + b * a.hist_ld;
     for (int i = tid; i < H; i += NT) {
-      const int id = hid[i];
+      const int id = (hist_rows && i == tid) ? hid0 : hid[i];
       if (id < 0 || id >= V) atomicOr(&sh.status, FL_ROW_BAD_HISTORY);
       else atomicOr(&hbits_dyn[id >> 5], 1u << (id & 31));
     }
