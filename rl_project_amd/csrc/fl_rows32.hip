@@ -883,17 +883,21 @@ __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xfor
   const bool sc = X.cap > 0.0f, tdiv = X.t > 0.0f;
   TopkHist h;
   if (X.pen) topk_hist_prefetch(S, X, V, h);
+  FL_MARK(16);
   uint32_t kt[TK_TILE][4], cmx[TK_TILE];
   bool bad = false;
   if (sc) topk_read1<true>(sh, S, X, V, q, kt, cmx, bad);
   else topk_read1<false>(sh, S, X, V, q, kt, cmx, bad);
   FL_MARK(1);
+  // (no barrier before the moves: they commute with read 1's adds, since the
+  // bin counters add modulo 2^32 and a count taken below zero is repaid by
+  // the adds still to come; nothing reads the bins before the barrier below)
   if (X.pen) {
-    __syncthreads();  // (every add of read 1 before the moves)
     FL_MARK(10);
     if (sc) topk_hist_move<true>(sh, S, X, V, h, bad);
     else topk_hist_move<false>(sh, S, X, V, h, bad);
   }
+  FL_MARK(13);
   __syncthreads();  // (every add and move before the scan reads the bins)
   FL_MARK(11);
 
@@ -1646,6 +1650,7 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
 __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   __shared__ Shared32 sh;
   extern __shared__ uint32_t hbits_dyn[];
+  FL_MARK(12);  // (kernel entry)
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int V = static_cast<int>(a.vocab);
@@ -1696,6 +1701,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
     for (int i = tid; i < (V + 31) / 32; i += NT) hbits_dyn[i] = 0;
   }
   __syncthreads();
+  FL_MARK(14);
   if (pen) {
     for (int i = tid; i < H; i += NT) {
       const int id = (hist_rows && i == tid) ? hid0 : hid[i];
@@ -1704,6 +1710,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
     }
   }
   __syncthreads();
+  FL_MARK(15);
 
   Xform X;
   X.cap = a.softcap;
