@@ -662,11 +662,29 @@ __device__ __forceinline__ uint32_t topk_count4(Shared32& sh, const Xform& X, in
   return max(max(k[0], k[1]), max(k[2], k[3]));
 }
 
-// The register tile: chunk u * NT + tid for u < TK_TILE, all loads in flight
-// at once (one memory round trip for rows up to 4 * TK_TILE * NT values),
-// issued before the row's history is read.
+// The register tile: chunk u * NT + tid for u < TK_TILE (one memory round
+// trip for rows up to 4 * TK_TILE * NT values).  Chunks U0 .. U1 - 1; a chunk
+// past the row reads 0 (the buffer's bound).  The first TK_EARLY go out before
+// the row's history is read, the rest after its barriers: a wave waits at a
+// barrier until the memory pipeline has taken every load it issued before
+// it (16 waves of 8 16-byte loads take ~0.85 us per CU).
+#ifndef FL_TK_EARLY
+#define FL_TK_EARLY 4
+#endif
+constexpr int TK_EARLY = FL_TK_EARLY;
+template <int U0, int U1>
 __device__ __forceinline__ void topk_tile_load(const Src& S, float4 (&q)[TK_TILE]) {
-  S.chunks(0, q);  // (past the row: 0, the buffer's bound)
+  const int tid = threadIdx.x;
+  if (S.aligned && (U1 * NT <= S.nfull || 4 * S.nfull == S.V)) {
+#pragma unroll
+    for (int u = U0; u < U1; ++u) {
+      const uint4 v = buf_load16(S.rs, 16u * static_cast<uint32_t>(u * NT + tid), 0u);
+      q[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    }
+  } else {
+#pragma unroll
+    for (int u = U0; u < U1; ++u) q[u] = S.chunk(u * NT + tid);
+  }
 }
 
 // Read 1: the register tile q (keys kept in kt, the largest of chunk u in
@@ -871,14 +889,16 @@ __device__ __forceinline__ void topk_init(Shared32& sh) {
   }
 }
 
-// The top-k path, after topk_init and topk_tile_load (q) and a barrier.
+// The top-k path, after topk_init, the tile's first TK_EARLY chunks and the
+// history barriers.
 // Returns false, with nothing decided, when the row needs another path.
 // Called by all threads (block-uniform control flow).
 __device__ __forceinline__ bool topk_path(Shared32& sh, const Src& S, const Xform& X, const RowCfg& R, RowOut& o,
-                                          const float4 (&q)[TK_TILE]) {
+                                          float4 (&q)[TK_TILE]) {
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
   const int V = R.V, K = R.K;
+  if constexpr (TK_EARLY < TK_TILE) topk_tile_load<TK_EARLY, TK_TILE>(S, q);
   if (sh.status != 0) return false;  // (rows with an error status: the two-read path reports them)
   const bool sc = X.cap > 0.0f, tdiv = X.t > 0.0f;
   TopkHist h;
@@ -1688,7 +1708,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   const bool topk_first = K > 0 && K < V && K <= TK_MAX;
   float4 q[TK_TILE];
   if (topk_first) {
-    topk_tile_load(S, q);
+    topk_tile_load<0, TK_EARLY>(S, q);
     topk_init(sh);
   }
 
