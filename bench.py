@@ -44,8 +44,9 @@ OTHER_CONFIGS = ("uniform_f32_64x32000", "softcap_zipf_f32_512x262144", "spec_f3
 
 
 def _traffic_from_profile(workload: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    scaled by the copy-kernel calibration), as recorded under profiles/ -- not
+    """HBM bytes per launch (per step, for a step of several kernels) measured
+    by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
+    calibration), as recorded under profiles/ -- not
     measured in this run (counters need a profiler run of their own).
     Returns (bytes or None, source description)."""
     rel = os.path.join("profiles", f"{workload}_traffic.txt")
@@ -54,7 +55,7 @@ def _traffic_from_profile(workload: str):
         return None, "no counter profile recorded for this workload"
     val, date = None, ""
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(("traffic_bytes_per_launch:", "traffic_bytes_per_step:")):
             val = float(line.split(":", 1)[1])
         elif line.startswith("measured:"):
             date = line.split(":", 1)[1].strip()
