@@ -545,21 +545,20 @@ __device__ __forceinline__ int fbin(float y, float c) {
 }
 // Upper bound of bin b's values (up to rounding).
 __device__ __forceinline__ float fub(int b, float c) { return c - static_cast<float>(b) * (1.0f / BPU); }
-// round(exp(y - ub_b) * 2^26) for y in bin b.  With u = (c - y) * 64, whose
-// integer part is b (fbin), y - ub_b = -fract(u) / 64 lies in (-1/64, 0]; the
-// degree-4 Taylor polynomial of exp(-f / 64) in f = fract(u) is exact to
-// 1e-11 there (one v_fract_f32 and four FMAs per value; rebuilding the bound
-// from b took four more), and t * 2^26 < 2^27 is an integer (t has 24
-// significant bits; at most 2^18 of them fit the bin word's 45-bit field).
+// exp(y - ub_b) * 2^26, truncated to an integer, for y in bin b.  With
+// u = (c - y) * 64, whose integer part is b (fbin), y - ub_b = -fract(u) / 64
+// lies in (-1/64, 0]; the degree-3 Taylor polynomial of exp(-f / 64) in
+// f = fract(u) is within 2.5e-9 of it there, 0.17 units of 2^-26 where the
+// float result's own unit is 4 of them (one v_fract_f32 and three FMAs per
+// value; rebuilding the bound from b took four more), and 2^18 terms of at
+// most 2^26 fit the bin word's 45-bit field.
 // Terms of the last bin are summed like the others (a value there is finite
 // or -inf, whose fraction is NaN and converts to 0) and dropped by fmass.
 // (The coefficients carry the factor 2^26: scaling by a power of two commutes
 // with each rounding of the Horner chain, so this is t * 2^26 exactly.)
 __device__ __forceinline__ uint32_t fterm(float y, float c) {
   const float f = __builtin_amdgcn_fractf((c - y) * BPU);
-  const float t26 = fmaf(f, fmaf(f, fmaf(f, fmaf(f, 67108864.0f / 402653184.0f, -67108864.0f / 1572864.0f),
-                                               67108864.0f / 8192.0f),
-                                 -67108864.0f / 64.0f),
+  const float t26 = fmaf(f, fmaf(f, fmaf(f, -67108864.0f / 1572864.0f, 67108864.0f / 8192.0f), -67108864.0f / 64.0f),
                          67108864.0f);
   return static_cast<uint32_t>(t26);
 }
