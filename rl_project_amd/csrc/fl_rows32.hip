@@ -133,6 +133,7 @@ struct Shared32 {
   int32_t result;
   uint32_t bcast_u;
   uint64_t bcast_q;
+  uint32_t grp[2];  // two-read path: next chunk group of read 1 and of read 2 (wave_groups)
 };
 
 // Element source: raw buffer loads of one row (range-checked, so loads past
@@ -175,7 +176,54 @@ struct Src {
       for (int u = 0; u < U; ++u) q[u] = chunk(c0 + u * NT + tid);
     }
   }
+  // The same for one wave: chunks base + u * WAVE + lane, u < U.
+  template <int U>
+  __device__ __forceinline__ void wchunks(int base, float4 (&q)[U]) const {
+    const int lane = threadIdx.x & (WAVE - 1);
+    if (aligned && (base + U * WAVE <= nfull || 4 * nfull == V)) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint4 v = buf_load16(rs, 16u * static_cast<uint32_t>(base + u * WAVE + lane), 0u);
+        q[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) q[u] = chunk(base + u * WAVE + lane);
+    }
+  }
 };
+
+// Chunk groups claimed wave by wave.  Group k holds chunks c_first +
+// 4 WAVE g + u WAVE + lane (u < 4) of the calling wave's lanes, with g = k,
+// or g = ng - 1 - k when last_first; a wave takes the next k from the LDS
+// counter `next` (zero before the first claim) until none is left, and calls
+// f(c, q) for each of its chunks (q: the chunk's 4 values, zeros past the
+// row).  The SIMDs favour older waves, so with a fixed share per wave the
+// youngest waves finish a read well after the oldest (16 us after them on
+// rows of 262144 values); claimed groups let the favoured waves take more,
+// and every wave ends within a group of the others.  For passes whose result
+// does not depend on which wave takes which chunk (bin sums, candidate lists
+// that are sorted afterwards).
+template <class F>
+__device__ __forceinline__ void wave_groups(const Src& S, uint32_t* next, int c_first, int ng, bool last_first,
+                                            F&& f) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  auto claim = [&]() -> int {
+    uint32_t k = 0;
+    if (lane == 0) k = atomicAdd(next, 1u);
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(k));
+  };
+  int k = claim();
+  while (k < ng) {
+    const int base = c_first + 4 * WAVE * (last_first ? ng - 1 - k : k);
+    float4 q[4];
+    S.wchunks(base, q);
+    const int kn = claim();  // (the next claim in flight with the loads)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) f(base + u * WAVE + lane, q[u]);
+    k = kn;
+  }
+}
 
 // Logit -> filtered value: soft-cap, repetition penalty (history elements),
 // temperature, each rounded to float32 as the reference's tensor ops round.
@@ -269,27 +317,6 @@ __device__ __forceinline__ void row_pass(const Src& S, const Xform& X, F&& f, in
       }
       // one chunk's elements at a time (interleaving all 16 costs VGPRs)
       __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-}
-
-// f(c, xs, hb) for every chunk c of the row, in groups of 4 NT chunks from the
-// last group to the first: its raw logits and history bits.
-template <class F>
-__device__ __forceinline__ void row_chunks_raw(const Src& S, const Xform& X, F&& f) {
-  const int tid = threadIdx.x;
-  const int nch = X.nch;
-  // (last chunks first: read 1 went first to last, so the bytes it read most
-  // recently, the likeliest still in the caches, are read again first;
-  // speculative rows 2.4 us faster per step, A/B on one box)
-  for (int c0 = nch > 0 ? ((nch - 1) / (4 * NT)) * (4 * NT) : -1; c0 >= 0; c0 -= 4 * NT) {
-    float4 q[4];
-    S.chunks(c0, q);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = c0 + u * NT + tid;
-      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-      f(c, xs, X.nibble(c));
     }
   }
 }
@@ -1160,20 +1187,15 @@ __device__ __forceinline__ bool read1(Shared32& sh, const Src& S, const Xform& X
     add4(u * NT + tid, y4);
   }
   const int nch = X.nch;
-  for (int c0 = 4 * NT; c0 < nch; c0 += 4 * NT) {
-    float4 q[4];
-    S.chunks(c0, q);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int ch = c0 + u * NT + tid;
-      const uint32_t hb = PEN ? X.nibble(ch) : 0u;
-      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-      float y4[4];
-      X.yt4<TDIV, PEN, SC>(xs, hb, y4);
-      add4(ch, y4);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
+  const int ng = nch > 4 * NT ? (nch - 4 * NT + 4 * WAVE - 1) / (4 * WAVE) : 0;
+  wave_groups(S, &sh.grp[0], 4 * NT, ng, false, [&](int ch, const float4& q) __attribute__((always_inline)) {
+    const uint32_t hb = PEN ? X.nibble(ch) : 0u;
+    const float xs[4] = {q.x, q.y, q.z, q.w};
+    float y4[4];
+    X.yt4<TDIV, PEN, SC>(xs, hb, y4);
+    add4(ch, y4);
+    __builtin_amdgcn_sched_barrier(0);
+  });
   return true;
 }
 
@@ -1475,7 +1497,13 @@ __device__ __forceinline__ bool two_read(Shared32& sh, const Src& S, const Xform
     auto stage = [&](auto pen_tag, auto nr_tag) __attribute__((always_inline)) {
       constexpr bool PEN = decltype(pen_tag)::value;
       constexpr int NR = decltype(nr_tag)::value;
-      row_chunks_raw(S, X, [&](int c, const float (&xs)[4], uint32_t hb) {
+      // (claimed groups, the row's last chunks first: read 1 went first to
+      // last, so the bytes it read most recently, the likeliest still in
+      // the caches, are read again first)
+      wave_groups(S, &sh.grp[1], 0, (X.nch + 4 * WAVE - 1) / (4 * WAVE), true,
+                  [&](int c, const float4& q) __attribute__((always_inline)) {
+        const float xs[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t hb = X.nibble(c);
         bool in[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1714,6 +1742,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   if (tid == 0) {
     sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
     sh.result = -1;
+    sh.grp[0] = sh.grp[1] = 0;
   }
   // ------------------------------------------------ history bitmap
   if (pen) {
