@@ -133,7 +133,7 @@ struct Shared32 {
   int32_t result;
   uint32_t bcast_u;
   uint64_t bcast_q;
-  uint32_t grp[2];  // two-read path: next chunk group of read 1 and of read 2 (wave_groups)
+  uint32_t grp[4];  // next chunk group (wave_groups): two-read path reads 1, 2; top-k path reads 1, 2
 };
 
 // Element source: raw buffer loads of one row (range-checked, so loads past
@@ -207,6 +207,7 @@ struct Src {
 template <class F>
 __device__ __forceinline__ void wave_groups(const Src& S, uint32_t* next, int c_first, int ng, bool last_first,
                                             F&& f) {
+  if (ng <= 0) return;  // (no claim: its LDS round trip would be the pass's only cost)
   const int lane = threadIdx.x & (WAVE - 1);
   auto claim = [&]() -> int {
     uint32_t k = 0;
@@ -725,15 +726,12 @@ __device__ __forceinline__ void topk_read1(Shared32& sh, const Src& S, const Xfo
     cmx[u] = topk_count4<SC>(sh, X, V, u * NT + tid, q[u], kt[u], bad);
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
-    float4 q[4];
-    S.chunks(c0, q);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      uint32_t k[4];
-      topk_count4<SC>(sh, X, V, c0 + u * NT + tid, q[u], k, bad);
-    }
-  }
+  // (past the tile: chunk groups claimed wave by wave, as in the two-read path)
+  const int ng = X.nch > TK_TILE * NT ? (X.nch - TK_TILE * NT + 4 * WAVE - 1) / (4 * WAVE) : 0;
+  wave_groups(S, &sh.grp[2], TK_TILE * NT, ng, false, [&](int ch, const float4& q) __attribute__((always_inline)) {
+    uint32_t k[4];
+    topk_count4<SC>(sh, X, V, ch, q, k, bad);
+  });
 }
 
 // History elements (bits of the bitmap X.hbits; thread t takes words t,
@@ -861,13 +859,10 @@ __device__ __forceinline__ void topk_read2(Shared32& sh, const Src& S, const Xfo
       }
     }
   }
-  for (int c0 = TK_TILE * NT; c0 < X.nch; c0 += 4 * NT) {
-    float4 q[4];
-    S.chunks(c0, q);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int ch = c0 + u * NT + tid;
-      const float xs[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+  // (past the tile: claimed chunk groups, the row's last chunks first)
+  const int ng = X.nch > TK_TILE * NT ? (X.nch - TK_TILE * NT + 4 * WAVE - 1) / (4 * WAVE) : 0;
+  wave_groups(S, &sh.grp[3], TK_TILE * NT, ng, true, [&](int ch, const float4& q) __attribute__((always_inline)) {
+      const float xs[4] = {q.x, q.y, q.z, q.w};
       uint32_t k[4], m = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -881,8 +876,7 @@ __device__ __forceinline__ void topk_read2(Shared32& sh, const Src& S, const Xfo
         for (int e = 0; e < 4; ++e)
           if ((m >> e) & 1u) topk_put(sh, pos, k[e], 4 * ch + e);
       }
-    }
-  }
+  });
   if (X.pen) {
     uint32_t m = 0;
 #pragma unroll
@@ -1742,7 +1736,7 @@ __global__ __launch_bounds__(NT) void k_sample_rows32(const fl_sample_args a) {
   if (tid == 0) {
     sh.status = hist_too_long ? FL_ROW_LIMIT : 0;
     sh.result = -1;
-    sh.grp[0] = sh.grp[1] = 0;
+    sh.grp[0] = sh.grp[1] = sh.grp[2] = sh.grp[3] = 0;
   }
   // ------------------------------------------------ history bitmap
   if (pen) {
