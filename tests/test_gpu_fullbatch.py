@@ -151,7 +151,9 @@ def test_reference_golden_vectors_through_the_gpu_dropin():
 def test_headline_launch_is_deterministic():
     """100 launches of the headline plan on fixed inputs: bit-identical tokens,
     log-probabilities and row descriptors (the kernels' LDS atomics and
-    barriers leave no order dependence)."""
+    barriers leave no order dependence); 50 of the float32 kernel on soft-capped
+    rows and on top-k rows of V=128256, whose reads hand chunk groups to
+    whichever wave claims them."""
     w = workloads.make("hetero_bf16_256x128256", seed=0).to("cuda")
     plan = SamplerPlan(w.logits, return_logprobs=True, return_desc=True, **w.kwargs())
     plan.launch()
@@ -175,3 +177,15 @@ def test_headline_launch_is_deterministic():
         p32.launch()
     torch.cuda.synchronize()
     assert torch.equal(p32.output.tokens, t1) and torch.equal(p32.output.desc, d1)
+    # and top-k rows longer than the float32 register tile (their streamed
+    # chunks go to whichever wave claims them)
+    wk = workloads.make("uniform_f32_64x32000", seed=2, batch=32, vocab=128256).to("cuda")
+    pk = SamplerPlan(wk.logits, return_logprobs=True, return_desc=True, **wk.kwargs())
+    pk.launch()
+    torch.cuda.synchronize()
+    t2, l2, d2 = pk.output.tokens.clone(), pk.output.logprobs.clone(), pk.output.desc.clone()
+    for i in range(50):
+        pk.launch()
+    torch.cuda.synchronize()
+    assert torch.equal(pk.output.tokens, t2) and torch.equal(pk.output.desc, d2)
+    assert torch.equal(pk.output.logprobs.view(torch.int32), l2.view(torch.int32))
